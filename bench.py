@@ -1,0 +1,309 @@
+"""Benchmark of the quantized MoE expert path on one MI355X.
+
+Headline workload (the metric's decode target): the
+Kimi-K2 MoE layer on one GPU's 48 local experts, 64 decode tokens, sigmoid
+top-8 routing from seeded N(0,1) logits -- router select, permutation,
+W13 grouped GEMM, SwiGLU, W2 grouped GEMM with routing weights, top-k combine.
+One step = one layer over resident inputs.  `value` is the layer's achieved
+HBM bandwidth over its algorithmic bytes (touched experts' weights + scales,
+activations in, routed output); the roofline block reports the dominant
+kernel (the W13 GEMM) timed with HIP events on its own stream inside the
+timed steps.  The other configurations (C1, C2, C4, C5) are reported under
+"configs"; the CPU baseline times the oracle's C restatement of the same
+layer on the host's cores.
+
+usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only c3]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = ("MoE layer µs + achieved HBM GB/s (decode) / MFMA TFLOP/s (prefill) on 1 MI355X")
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+W13_BYTES_PER_EXPERT = 4096 * 7168 // 2 + 4096 * (7168 // 32) * 2  # 16,515,072
+W2_BYTES_PER_EXPERT = 7168 * 2048 // 2 + 7168 * (2048 // 32) * 2  # 8,257,536
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--only", default="", help="comma list of configs to run (c1..c5)")
+    return p.parse_args()
+
+
+class EventTimer:
+    """Pairs of HIP events recorded on the stream the kernels run on."""
+
+    def __init__(self, torch):
+        self.torch = torch
+        self.pairs = []
+
+    def start(self):
+        e = self.torch.cuda.Event(enable_timing=True)
+        e.record(self.torch.cuda.current_stream())
+        return e
+
+    def stop(self, s):
+        e = self.torch.cuda.Event(enable_timing=True)
+        e.record(self.torch.cuda.current_stream())
+        self.pairs.append((s, e))
+
+    def mean_ms(self):
+        self.torch.cuda.synchronize()
+        if not self.pairs:
+            return float("nan")
+        return sum(s.elapsed_time(e) for s, e in self.pairs) / len(self.pairs)
+
+
+def time_steps(torch, fn, steps, warmup):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / steps
+
+
+def dev(torch, a, bf16=False):
+    import numpy as np
+    a = np.ascontiguousarray(a)
+    if bf16:
+        return torch.from_numpy(a.view(np.int16)).cuda().view(torch.bfloat16)
+    return torch.from_numpy(a).cuda()
+
+
+# ----------------------------------------------------------------------------- C3
+def bench_c3(torch, args, results):
+    import numpy as np
+    from pegainfer_amd import layer, ops, synth
+    E, H, I, T = 48, 7168, 2048, 64
+    log("C3: generating 48 experts (seeded) and packing on the GPU")
+    g = synth.rng(3, 1)
+    gate, up, down = (synth.int4_checkpoint(g, E, I, H), synth.int4_checkpoint(g, E, I, H),
+                      synth.int4_checkpoint(g, E, H, I))
+    hidden_np = synth.normal_bf16(synth.rng(3, 2), (T, H))
+    logits_np = synth.rng(3, 3).standard_normal((T, 384), dtype=np.float32)
+    bs = ops.kimi_marlin_block_size(T)
+    moe = layer.RoutedExperts(layer.package_w13(gate, up), layer.package_projection(*down),
+                              max_tokens=T, topk=8, block_size=bs)
+    hidden = dev(torch, hidden_np, bf16=True)
+    logits = dev(torch, logits_np)
+    bias = torch.zeros(384, dtype=torch.float32, device="cuda")
+    tw = torch.zeros(T, 8, dtype=torch.float32, device="cuda")
+    ti = torch.zeros(T, 8, dtype=torch.int32, device="cuda")
+    out = torch.zeros(T, H, dtype=torch.float32, device="cuda")
+    timer = EventTimer(torch)
+
+    def step(record=False):
+        ops.kimi_router_select(logits, bias, tw, ti, T)
+        moe.forward(hidden, ti, tw, out, w13_timer=timer if record else None)
+
+    step()
+    torch.cuda.synchronize()
+    idx = ti.cpu().numpy()
+    touched = np.unique(idx[idx < E]).size
+    local_routes = int((idx < E).sum())
+    alg_bytes = (touched * (W13_BYTES_PER_EXPERT + W2_BYTES_PER_EXPERT) + T * H * 2 + T * H * 4)
+    w13_bytes = touched * W13_BYTES_PER_EXPERT + T * H * 2 + local_routes * 2 * I * 2
+    log(f"C3: block size {bs}, {touched} experts touched, {local_routes} local routes, "
+        f"{alg_bytes / 1e6:.1f} MB algorithmic")
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step(record=True)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    w13_ms = timer.mean_ms()
+    results["c3"] = dict(
+        workload="c3_kimi_moe_decode_t64", tokens=T, local_experts=E, hidden=H, inter=I, topk=8,
+        block_size=bs, touched_experts=touched, local_routes=local_routes,
+        algorithmic_bytes=alg_bytes, layer_us=ms * 1e3,
+        layer_gbs=alg_bytes / (ms * 1e-3) / 1e9, w13_us=w13_ms * 1e3,
+        w13_algorithmic_bytes=w13_bytes, w13_gbs=w13_bytes / (w13_ms * 1e-3) / 1e9)
+    log(f"C3: layer {ms * 1e3:.1f} us ({results['c3']['layer_gbs']:.0f} GB/s), "
+        f"W13 {w13_ms * 1e3:.1f} us ({results['c3']['w13_gbs']:.0f} GB/s)")
+    return dict(gate=gate, up=up, down=down, hidden=hidden_np, idx=idx,
+                w=tw.cpu().numpy(), bs=bs, alg_bytes=alg_bytes)
+
+
+def cpu_baseline_c3(ctx, results):
+    """The oracle (C, -O3, pthreads) running the same C3 layer on host cores."""
+    import numpy as np
+    from oracle import oracle
+    threads = min(16, os.cpu_count() or 1)
+    w13p = np.concatenate([ctx["gate"][0], ctx["up"][0]], axis=1)
+    w13s = np.concatenate([ctx["gate"][1], ctx["up"][1]], axis=1)
+    runs, t_total = 0, 0.0
+    while runs < 3 and t_total < 20.0:
+        t0 = time.perf_counter()
+        oracle.kimi_moe_layer(ctx["hidden"], w13p, w13s, ctx["down"][0], ctx["down"][1],
+                              ctx["idx"].reshape(-1), ctx["w"], global_start=0, local_experts=48,
+                              block_size=ctx["bs"], hidden=7168, inter=2048, threads=threads)
+        t_total += time.perf_counter() - t0
+        runs += 1
+    sec = t_total / runs
+    results["cpu"] = dict(value=ctx["alg_bytes"] / sec / 1e9, unit="GB/s", cores=threads,
+                          kind="port", sample=f"{runs} full C3 layers (64 tokens, 48 experts)",
+                          layer_ms=sec * 1e3)
+    log(f"CPU baseline: {sec * 1e3:.0f} ms per layer on {threads} threads")
+
+
+# ----------------------------------------------------------------------------- C1/C2
+def bench_c1(torch, args, results):
+    from pegainfer_amd import layer, synth
+    g = synth.rng(1, 1)
+    packed, scales = synth.int4_checkpoint(g, 1, 9728, 2560)
+    dense = layer.DenseW4A16(layer.package_projection(packed, scales), max_rows=1)
+    x = dev(torch, synth.normal_bf16(synth.rng(1, 2), (1, 2560)), bf16=True)
+    y = torch.zeros(1, 9728, dtype=torch.bfloat16, device="cuda")
+    ms = time_steps(torch, lambda: dense.forward(x, y), max(args.steps, 200), args.warmup)
+    b = 14_032_896
+    results["c1"] = dict(workload="c1_dense_gemv_9728x2560", us=ms * 1e3,
+                         gbs=b / (ms * 1e-3) / 1e9, algorithmic_bytes=b)
+    log(f"C1: {ms * 1e3:.2f} us ({results['c1']['gbs']:.0f} GB/s)")
+
+
+def bench_c2(torch, args, results):
+    from pegainfer_amd import layer, synth
+    g = synth.rng(2, 1)
+    gate, up, down = (synth.int4_checkpoint(g, 1, 2048, 7168), synth.int4_checkpoint(g, 1, 2048, 7168),
+                      synth.int4_checkpoint(g, 1, 7168, 2048))
+    ffn = layer.ExpertFFN(layer.package_w13(gate, up), layer.package_projection(*down), max_rows=8)
+    out = {}
+    for b in (1, 4, 8):
+        x = dev(torch, synth.normal_bf16(synth.rng(2, 2), (b, 7168)), bf16=True)
+        y = torch.zeros(b, 7168, dtype=torch.bfloat16, device="cuda")
+        ms = time_steps(torch, lambda: ffn.forward(x, y), max(args.steps, 200), args.warmup)
+        nbytes = W13_BYTES_PER_EXPERT + W2_BYTES_PER_EXPERT + b * 7168 * 4
+        out[f"b{b}"] = dict(us=ms * 1e3, gbs=nbytes / (ms * 1e-3) / 1e9)
+        log(f"C2 b={b}: {ms * 1e3:.2f} us ({out[f'b{b}']['gbs']:.0f} GB/s)")
+    results["c2"] = dict(workload="c2_kimi_expert_ffn", **out)
+
+
+# ----------------------------------------------------------------------------- C4/C5
+def bench_c4(torch, args, results):
+    import numpy as np
+    from pegainfer_amd import layer, ops, synth
+    E, H, I, T, topk = 64, 2048, 1408, 512, 6
+    g = synth.rng(4, 1)
+    gate, up, down = (synth.int4_checkpoint(g, E, I, H), synth.int4_checkpoint(g, E, I, H),
+                      synth.int4_checkpoint(g, E, H, I))
+    sg, su, sd = (synth.int4_checkpoint(g, 1, 2 * I, H), synth.int4_checkpoint(g, 1, 2 * I, H),
+                  synth.int4_checkpoint(g, 1, H, 2 * I))
+    bs = ops.kimi_marlin_block_size(T, topk=topk, local_experts=E)
+    routed = layer.RoutedExperts(layer.package_w13(gate, up), layer.package_projection(*down),
+                                 max_tokens=T, topk=topk, block_size=bs)
+    shared = layer.ExpertFFN(layer.package_w13(sg, su), layer.package_projection(*sd), max_rows=T)
+    moe = layer.Dsv2MoeLayer(routed, shared)
+    hidden = dev(torch, synth.normal_bf16(synth.rng(4, 2), (T, H)), bf16=True)
+    logits = dev(torch, synth.rng(4, 3).standard_normal((T, E), dtype=np.float32))
+    out = torch.zeros(T, H, dtype=torch.bfloat16, device="cuda")
+    ms = time_steps(torch, lambda: moe.forward(hidden, logits, out), args.steps, args.warmup)
+    flops = 2 * T * topk * (2 * I * H + H * I) + 2 * T * (2 * 2 * I * H + H * 2 * I)
+    results["c4"] = dict(workload="c4_dsv2lite_moe_prefill_t512", us=ms * 1e3,
+                         tflops=flops / (ms * 1e-3) / 1e12, flops=flops, block_size=bs)
+    log(f"C4: {ms * 1e3:.1f} us ({results['c4']['tflops']:.1f} TFLOP/s)")
+
+
+def bench_c5(torch, args, results):
+    from pegainfer_amd import layer, ops, synth
+    E, H, I, T = 48, 7168, 2048, 4096
+    g = synth.rng(5, 1)
+    gate, up, down = (synth.int4_checkpoint(g, E, I, H), synth.int4_checkpoint(g, E, I, H),
+                      synth.int4_checkpoint(g, E, H, I))
+    idx, w = synth.zipf_local_topk(synth.rng(5, 3), T)
+    routes = int((idx < E).sum())
+    bs = ops.kimi_marlin_block_size(T)
+    moe = layer.RoutedExperts(layer.package_w13(gate, up), layer.package_projection(*down),
+                              max_tokens=T, topk=8, block_size=bs)
+    hidden = dev(torch, synth.normal_bf16(synth.rng(5, 2), (T, H)), bf16=True)
+    ti, tw = dev(torch, idx), dev(torch, w)
+    out = torch.zeros(T, H, dtype=torch.float32, device="cuda")
+    timer = EventTimer(torch)
+    ms = time_steps(torch, lambda: moe.forward(hidden, ti, tw, out, w13_timer=timer),
+                    max(5, args.steps // 5), 2)
+    w13_ms = timer.mean_ms()
+    flops = 2 * routes * (2 * I * H + H * I)
+    w13_flops = 2 * routes * 2 * I * H
+    results["c5"] = dict(workload="c5_kimi_prefill_t4096_zipf", routes=routes, us=ms * 1e3,
+                         tflops=flops / (ms * 1e-3) / 1e12, flops=flops,
+                         w13_us=w13_ms * 1e3, w13_tflops=w13_flops / (w13_ms * 1e-3) / 1e12)
+    log(f"C5: R={routes}, layer {ms * 1e3:.1f} us ({results['c5']['tflops']:.1f} TFLOP/s), "
+        f"W13 {w13_ms * 1e3:.1f} us ({results['c5']['w13_tflops']:.1f} TFLOP/s)")
+
+
+def load_traffic(name):
+    path = os.path.join(ROOT, "profiles", f"traffic_{name}.json")
+    if os.path.exists(path):
+        with open(path) as f:
+            return json.load(f).get("hbm_bytes_per_launch")
+    return None
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only (no multi-GPU path); "
+                                   "run with --gpus 1"}))
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU visible"}))
+        sys.exit(2)
+    torch.cuda.set_device(0)
+    import pegainfer_amd
+    pegainfer_amd.load()
+    only = set(x.strip() for x in args.only.split(",") if x.strip())
+    want = lambda c: not only or c in only  # noqa: E731
+    results = {}
+    ctx = bench_c3(torch, args, results)
+    for name, fn in (("c1", bench_c1), ("c2", bench_c2), ("c4", bench_c4), ("c5", bench_c5)):
+        if want(name):
+            fn(torch, args, results)
+    if not args.no_cpu:
+        cpu_baseline_c3(ctx, results)
+    c3 = results["c3"]
+    roof = dict(bound="hbm", kernel="wna16_decode_kernel (W13, C3)",
+                achieved=round(c3["w13_gbs"], 1), peak=HBM_PEAK_GBS, unit="GB/s",
+                frac=round(c3["w13_gbs"] / HBM_PEAK_GBS, 4),
+                traffic=load_traffic("wna16_w13_c3"),
+                algorithmic_bytes_per_launch=c3["w13_algorithmic_bytes"],
+                launch_us=round(c3["w13_us"], 2))
+    line = dict(
+        metric=METRIC, value=round(c3["layer_gbs"], 1), unit="GB/s", n_gpus=1, steps=args.steps,
+        warmup=args.warmup, ms_per_step=round(c3["layer_us"] / 1e3, 5), higher_is_better=True,
+        scaling="weak", vs_baseline=None, dtype="bf16",
+        data="synthetic (seeded INT4 weights / bf16 N(0,1) activations / N(0,1) router logits)",
+        config=dict(workload=c3["workload"], tokens=64, local_experts=48, hidden=7168, inter=2048,
+                    topk=8, block_size=c3["block_size"], touched_experts=c3["touched_experts"],
+                    layer_us=round(c3["layer_us"], 2),
+                    algorithmic_bytes=c3["algorithmic_bytes"]),
+        roofline=roof,
+        cpu_baseline=None if "cpu" not in results else {
+            k: (round(v, 3) if isinstance(v, float) else v) for k, v in results["cpu"].items()},
+        configs={k: v for k, v in results.items() if k not in ("cpu",)},
+    )
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

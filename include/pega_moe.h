@@ -1,0 +1,181 @@
+/*
+ * pega_moe.h -- C ABI of libpega_moe_hip.so, the MI355X (gfx950) quantized
+ * MoE expert path (W4A16: INT4 group-32 symmetric weights, bf16 activations,
+ * fp32 accumulation).
+ *
+ * Conventions (as in the reference's FFI, pegainfer-kernels/src/ffi/kimi.rs
+ * and src/ffi.rs:5):
+ *   - bf16 tensors are passed as uint16_t bit patterns;
+ *   - all pointers are device pointers, caller-owned; no entry point
+ *     allocates, synchronises or copies to the host;
+ *   - `stream` is a hipStream_t (the reference passes a CUstream);
+ *   - return value: 0 success, 1 invalid value, 801 not supported,
+ *     719 launch failed (CUresult numbering); the reason for the last
+ *     non-zero return on the calling thread is pegainfer_kernels_last_error().
+ *
+ * Entry points named kimi_* keep the reference's symbol names, argument order
+ * and shape guards (48 local experts, top-8, group 32), so they are drop-in
+ * replacements.  Entry points named pega_* have no reference counterpart:
+ * they are the shape-general forms (any expert count / top-k) used for the
+ * dense and DeepSeek-V2-Lite-shaped configurations, plus the routing select
+ * stages the reference runs inside larger calls or on the host.
+ */
+#ifndef PEGA_MOE_H_
+#define PEGA_MOE_H_
+
+#include <stdbool.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* hipStream_t;
+
+/* Reason for the last failure on this thread (never NULL).
+ * Replaces: pegainfer_kernels_last_error, pegainfer-kernels/csrc/shared/ffi_last_error.cu:13 */
+const char* pegainfer_kernels_last_error(void);
+
+/* ---------------- token -> expert permutation ---------------- */
+
+/* Replaces kimi_moe_marlin_align_block_size_cuda, pegainfer-kernels/src/ffi/kimi.rs:279-294
+ * (csrc/kimi_k2/kimi_experts.cu:197-268).  Deterministic for every route count. */
+int kimi_moe_marlin_align_block_size_cuda(const int32_t* topk_idx, int32_t* sorted_token_ids,
+                                          int32_t* expert_ids, int32_t* num_tokens_post_padded,
+                                          uint32_t* expert_offsets, uint32_t* expert_cursor,
+                                          int active_tokens, int topk, int global_start,
+                                          int local_experts, int block_size,
+                                          int max_padded_tokens, int max_m_blocks,
+                                          hipStream_t stream);
+
+/* No reference counterpart: shape-general form of the call above (local_experts <= 224,
+ * any topk). */
+int pega_moe_align_block_size(const int32_t* topk_idx, int32_t* sorted_token_ids,
+                              int32_t* expert_ids, int32_t* num_tokens_post_padded,
+                              uint32_t* expert_offsets, uint32_t* expert_cursor,
+                              int active_tokens, int topk, int global_start, int local_experts,
+                              int block_size, int max_padded_tokens, int max_m_blocks,
+                              hipStream_t stream);
+
+/* Replaces kimi_deepep_build_marlin_routing_on_stream, pegainfer-kernels/src/ffi/kimi.rs:296-307
+ * (csrc/kimi_k2/kimi_experts.cu:435-459). */
+int kimi_deepep_build_marlin_routing_on_stream(const int32_t* psum_expert,
+                                               int32_t* sorted_token_ids, int32_t* expert_ids,
+                                               int32_t* num_tokens_post_padded,
+                                               int num_local_experts, int alignment,
+                                               int block_size, int max_padded_tokens,
+                                               int max_m_blocks, hipStream_t stream);
+
+/* ---------------- load-time weight packaging (Marlin layout, bit-exact) ---------------- */
+
+/* Replaces kimi_marlin_int4_reorder_weight_cuda, pegainfer-kernels/src/ffi/kimi.rs:93-101. */
+int kimi_marlin_int4_reorder_weight_cuda(const uint8_t* weight_packed_checkpoint,
+                                         uint8_t* weight_packed_marlin, int in_dim, int out_dim,
+                                         int local_experts, int group_size, hipStream_t stream);
+
+/* Replaces kimi_marlin_int4_reorder_scale_cuda, pegainfer-kernels/src/ffi/kimi.rs:84-91. */
+int kimi_marlin_int4_reorder_scale_cuda(const uint16_t* weight_scale_checkpoint,
+                                        uint16_t* weight_scale_marlin, int in_dim, int out_dim,
+                                        int local_experts, int group_size, hipStream_t stream);
+
+/* Replaces kimi_marlin_int4_fuse_w13_cuda, pegainfer-kernels/src/ffi/kimi.rs:68-82. */
+int kimi_marlin_int4_fuse_w13_cuda(const uint8_t* gate_weight_packed_marlin,
+                                   const uint8_t* up_weight_packed_marlin,
+                                   uint8_t* w13_weight_packed_marlin,
+                                   const uint16_t* gate_scale_marlin,
+                                   const uint16_t* up_scale_marlin, uint16_t* w13_scale_marlin,
+                                   int in_dim, int intermediate_dim, int local_experts,
+                                   int group_size, hipStream_t stream);
+
+/* No reference counterpart: the three calls above for any expert count. */
+int pega_marlin_int4_reorder_weight(const uint8_t* ckpt, uint8_t* marlin, int in_dim,
+                                    int out_dim, int local_experts, int group_size,
+                                    hipStream_t stream);
+int pega_marlin_int4_reorder_scale(const uint16_t* ckpt, uint16_t* marlin, int in_dim,
+                                   int out_dim, int local_experts, int group_size,
+                                   hipStream_t stream);
+int pega_marlin_int4_fuse_w13(const uint8_t* gate_w, const uint8_t* up_w, uint8_t* w13_w,
+                              const uint16_t* gate_s, const uint16_t* up_s, uint16_t* w13_s,
+                              int in_dim, int intermediate_dim, int local_experts,
+                              int group_size, hipStream_t stream);
+
+/* ---------------- grouped W4A16 GEMM ---------------- */
+
+/* Replaces kimi_marlin_wna16_gemm_cuda, pegainfer-kernels/src/ffi/kimi.rs:131-152
+ * (csrc/kimi_k2/kimi_marlin_wna16.cu:241-343,414-442).  c_tmp follows the reference's
+ * sizing (size_n * sorted_token_ids_len floats, x2 for block size 8); workspace (locks)
+ * is left all-zero on return. */
+int kimi_marlin_wna16_gemm_cuda(const uint16_t* input, uint16_t* output, float* c_tmp,
+                                const uint8_t* b_qweight, const uint16_t* b_scales,
+                                int32_t* workspace, const int32_t* sorted_token_ids,
+                                const int32_t* expert_ids, const int32_t* num_tokens_post_padded,
+                                const float* topk_weights, int workspace_len,
+                                int sorted_token_ids_len, int moe_block_size, int top_k,
+                                bool mul_topk_weights, int size_m, int size_n, int size_k,
+                                int local_experts, int group_size, int sm_count,
+                                hipStream_t stream);
+
+/* No reference counterpart: shape-general form with an explicit c_tmp length (floats). */
+int pega_wna16_gemm(const uint16_t* input, uint16_t* output, float* c_tmp, long long c_tmp_len,
+                    const uint8_t* b_qweight, const uint16_t* b_scales, int32_t* workspace,
+                    int workspace_len, const int32_t* sorted_token_ids, const int32_t* expert_ids,
+                    const int32_t* num_tokens_post_padded, const float* topk_weights,
+                    int sorted_token_ids_len, int moe_block_size, int top_k,
+                    bool mul_topk_weights, int size_m, int size_n, int size_k, int local_experts,
+                    int group_size, int sm_count, hipStream_t stream);
+
+/* ---------------- activation / combine / residual ---------------- */
+
+/* Replaces kimi_marlin_w13_swiglu_cuda, pegainfer-kernels/src/ffi/kimi.rs:113-119. */
+int kimi_marlin_w13_swiglu_cuda(const uint16_t* w13, uint16_t* out, int rows,
+                                int intermediate_dim, hipStream_t stream);
+
+/* Replaces kimi_marlin_w13_swiglu_expanded_cuda, pegainfer-kernels/src/ffi/kimi.rs:121-129. */
+int kimi_marlin_w13_swiglu_expanded_cuda(const uint16_t* w13, uint16_t* out,
+                                         const int32_t* num_tokens_post_padded, int max_rows,
+                                         int intermediate_dim, int sm_count, hipStream_t stream);
+
+/* Replaces kimi_marlin_sum_topk_rows_f32_cuda, pegainfer-kernels/src/ffi/kimi.rs:104-111. */
+int kimi_marlin_sum_topk_rows_f32_cuda(const uint16_t* route_output, float* out,
+                                       int active_tokens, int topk, int hidden_dim,
+                                       hipStream_t stream);
+
+/* No reference C symbol: the DeepSeek-V2-Lite weighted fp32 combine (fmaf chain in route
+ * order), restating pegainfer-kernels/csrc/deepseek_v2_lite/dsv2_lite_moe.cu:131-155. */
+int pega_weighted_topk_sum_f32(const uint16_t* route_output, const float* topk_weight,
+                               float* out, int active_tokens, int topk, int hidden_dim,
+                               hipStream_t stream);
+
+/* Replaces kimi_residual_add_scaled_f32_cuda, pegainfer-kernels/src/ffi/kimi.rs:309-317. */
+int kimi_residual_add_scaled_f32_cuda(const uint16_t* hidden, const uint16_t* projected,
+                                      const float* routed_f32, float scale, uint16_t* out, int n,
+                                      hipStream_t stream);
+
+/* Replaces kimi_residual_add_scaled_bf16_cuda, pegainfer-kernels/src/ffi/kimi.rs:319-327. */
+int kimi_residual_add_scaled_bf16_cuda(const uint16_t* hidden, const uint16_t* projected,
+                                       const uint16_t* routed, float scale, uint16_t* out, int n,
+                                       hipStream_t stream);
+
+/* Replaces kimi_add_f32_bf16_to_bf16_cuda, pegainfer-kernels/src/ffi/kimi.rs:9-15. */
+int kimi_add_f32_bf16_to_bf16_cuda(const float* a, const uint16_t* b, uint16_t* out, int n,
+                                   hipStream_t stream);
+
+/* ---------------- routing select ---------------- */
+
+/* No reference symbol of its own: the select stage (sigmoid, top-k of score+bias, renormalise)
+ * of kimi_k2_router_noaux_tc_cuda, pegainfer-kernels/src/ffi/kimi.rs:52-66
+ * (csrc/kimi_k2/kimi_router.cu:20-91), taking precomputed fp32 logits. */
+int pega_kimi_router_select(const float* logits, const float* e_score_correction_bias,
+                            float* topk_weight, int32_t* topk_idx, int active_tokens,
+                            int n_experts, int topk, float route_scale, hipStream_t stream);
+
+/* No reference C symbol: DeepSeek-V2-Lite softmax top-k sorted by expert id, restating
+ * pegainfer-deepseek-v2-lite/src/host_ops.rs:388-412. */
+int pega_dsv2_router_select(const float* logits, float* topk_weight, int32_t* topk_idx,
+                            int tokens, int n_experts, int topk, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PEGA_MOE_H_ */

@@ -1,0 +1,70 @@
+// Shared definitions of the MI355X (gfx950) quantized-MoE expert-path library.
+//
+// ABI conventions (mirroring pegainfer-kernels/src/ffi/kimi.rs and src/ffi.rs:5):
+//   * bf16 tensors cross the boundary as uint16_t bit patterns;
+//   * every entry point returns an int with CUresult-compatible values;
+//   * entry points never allocate, never synchronise and never throw; the
+//     reason for a non-zero return is kept in a thread-local string that
+//     pegainfer_kernels_last_error() returns (csrc/shared/ffi_last_error.cu:13
+//     in the reference).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define PEGA_API extern "C" __attribute__((visibility("default")))
+
+namespace pega {
+
+// CUresult-compatible status codes (cudarc::driver::sys::CUresult values).
+enum Status : int {
+  kSuccess = 0,
+  kInvalidValue = 1,
+  kNotInitialized = 3,
+  kNotSupported = 801,
+  kLaunchFailed = 719,
+};
+
+// Records the reason for a failure (printf-style) and returns `code`.
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+
+// Maps the launch status of the kernel just enqueued to a Status.
+int launch_status(const char* what);
+
+// Number of compute units of the current device (cached per device).
+int current_cu_count();
+
+// ---------------------------------------------------------------- bf16 helpers
+__device__ __forceinline__ float bf2f(uint16_t h) {
+  return __builtin_bit_cast(float, static_cast<uint32_t>(h) << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16 (v_cvt_pk_bf16_f32 on gfx950).
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+}
+
+// Two fp32 -> packed bf16 pair (lo = a, hi = b), one v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2_t;
+  bf16x2_t v;
+  v[0] = static_cast<__bf16>(a);
+  v[1] = static_cast<__bf16>(b);
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+__device__ __forceinline__ float bf_lo(uint32_t p) { return __builtin_bit_cast(float, p << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t p) {
+  return __builtin_bit_cast(float, p & 0xffff0000u);
+}
+
+// e^x as the correctly rounded float of a double-precision exp.  Used where
+// the reference calls expf and the result decides an index (router scores);
+// the CPU checker uses the same definition.
+__device__ __forceinline__ float exp_exact_f32(float x) {
+  return static_cast<float>(::exp(static_cast<double>(x)));
+}
+
+__host__ __device__ constexpr int ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+}  // namespace pega

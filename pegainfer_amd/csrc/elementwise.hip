@@ -1,0 +1,276 @@
+// Bandwidth-bound stages of the expert path: SwiGLU, top-k row sums and the
+// residual joins.  Each kernel restates the reference's rounding points
+// exactly and moves 16 bytes per lane per access where shapes allow.
+//
+//   kimi_marlin_w13_swiglu_cuda           kimi_marlin_wna16.cu:345-361,444-460
+//   kimi_marlin_w13_swiglu_expanded_cuda  kimi_marlin_wna16.cu:367-390,462-493
+//   kimi_marlin_sum_topk_rows_f32_cuda    kimi_marlin_wna16.cu:392-408,495-513
+//   kimi_residual_add_scaled_f32_cuda     kimi_experts.cu:25-39,287-306
+//   kimi_residual_add_scaled_bf16_cuda    kimi_experts.cu:308-346
+//   kimi_add_f32_bf16_to_bf16_cuda        kimi_experts.cu:15-23,270-285
+//   pega_weighted_topk_sum_f32            dsv2_lite_moe.cu:131-155 (fmaf chain)
+#include "common.h"
+
+namespace pega {
+namespace {
+
+// out = bf16( f(bf16(g / (1 + e^-g))) * u ), g = gate column, u = up column.
+__device__ __forceinline__ uint16_t swiglu_one(float g, float u) {
+  const float e = (g == 0.0f) ? 1.0f : exp_exact_f32(-g);
+  const float silu = g / (1.0f + e);
+  return f2bf(bf2f(f2bf(silu)) * u);
+}
+
+__device__ __forceinline__ void swiglu8(const uint16_t* __restrict__ row, uint16_t* __restrict__ out,
+                                        int inter, int c8) {
+  const uint4 g = *reinterpret_cast<const uint4*>(row + c8);
+  const uint4 u = *reinterpret_cast<const uint4*>(row + inter + c8);
+  const uint32_t gw[4] = {g.x, g.y, g.z, g.w}, uw[4] = {u.x, u.y, u.z, u.w};
+  uint32_t ow[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    uint16_t lo = swiglu_one(bf_lo(gw[i]), bf_lo(uw[i]));
+    uint16_t hi = swiglu_one(bf_hi(gw[i]), bf_hi(uw[i]));
+    ow[i] = static_cast<uint32_t>(lo) | (static_cast<uint32_t>(hi) << 16);
+  }
+  *reinterpret_cast<uint4*>(out + c8) = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+}
+
+// rows read from `rows_ptr` (device) when non-null, clamped to max_rows.
+__global__ void swiglu_vec_kernel(const uint16_t* __restrict__ w13, uint16_t* __restrict__ out,
+                                  int rows, const int32_t* __restrict__ rows_ptr, int inter) {
+  int nrows = rows;
+  if (rows_ptr) {
+    nrows = rows_ptr[0];
+    if (nrows <= 0) return;
+    if (nrows > rows) nrows = rows;
+  }
+  const int per_row = inter >> 3;
+  const long long total = static_cast<long long>(nrows) * per_row;
+  for (long long idx = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
+       idx += static_cast<long long>(gridDim.x) * blockDim.x) {
+    const long long r = idx / per_row;
+    const int c8 = static_cast<int>(idx - r * per_row) * 8;
+    swiglu8(w13 + r * 2 * inter, out + r * inter, inter, c8);
+  }
+}
+
+__global__ void swiglu_scalar_kernel(const uint16_t* __restrict__ w13, uint16_t* __restrict__ out,
+                                     int rows, const int32_t* __restrict__ rows_ptr, int inter) {
+  int nrows = rows;
+  if (rows_ptr) {
+    nrows = rows_ptr[0];
+    if (nrows <= 0) return;
+    if (nrows > rows) nrows = rows;
+  }
+  const long long total = static_cast<long long>(nrows) * inter;
+  for (long long idx = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
+       idx += static_cast<long long>(gridDim.x) * blockDim.x) {
+    const long long r = idx / inter;
+    const int c = static_cast<int>(idx - r * inter);
+    const uint16_t* row = w13 + r * 2 * inter;
+    out[idx] = swiglu_one(bf2f(row[c]), bf2f(row[inter + c]));
+  }
+}
+
+// out[t, d] = ((0 + r0) + r1) + ... + r_{topk-1}  (fp32, k ascending).
+__global__ void sum_topk_vec_kernel(const uint16_t* __restrict__ route, float* __restrict__ out,
+                                    int tokens, int topk, int hidden) {
+  const int per_row = hidden >> 3;
+  const long long total = static_cast<long long>(tokens) * per_row;
+  for (long long idx = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
+       idx += static_cast<long long>(gridDim.x) * blockDim.x) {
+    const long long t = idx / per_row;
+    const int d8 = static_cast<int>(idx - t * per_row) * 8;
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int k = 0; k < topk; ++k) {
+      const uint4 v = *reinterpret_cast<const uint4*>(route + (t * topk + k) * hidden + d8);
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[2 * i] += bf_lo(w[i]);
+        acc[2 * i + 1] += bf_hi(w[i]);
+      }
+    }
+    float4* o = reinterpret_cast<float4*>(out + t * hidden + d8);
+    o[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    o[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+  }
+}
+
+__global__ void sum_topk_scalar_kernel(const uint16_t* __restrict__ route, float* __restrict__ out,
+                                       int tokens, int topk, int hidden) {
+  const long long total = static_cast<long long>(tokens) * hidden;
+  for (long long idx = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
+       idx += static_cast<long long>(gridDim.x) * blockDim.x) {
+    const long long t = idx / hidden;
+    const int d = static_cast<int>(idx - t * hidden);
+    float acc = 0.0f;
+    for (int k = 0; k < topk; ++k) acc += bf2f(route[(t * topk + k) * hidden + d]);
+    out[idx] = acc;
+  }
+}
+
+// out[t, d] = fma(f(r_k), w[t, k], ...) for k ascending, starting from 0.
+__global__ void weighted_topk_sum_kernel(const uint16_t* __restrict__ route,
+                                         const float* __restrict__ topk_weight,
+                                         float* __restrict__ out, int tokens, int topk,
+                                         int hidden) {
+  const long long total = static_cast<long long>(tokens) * hidden;
+  for (long long idx = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
+       idx += static_cast<long long>(gridDim.x) * blockDim.x) {
+    const long long t = idx / hidden;
+    const int d = static_cast<int>(idx - t * hidden);
+    float acc = 0.0f;
+    for (int k = 0; k < topk; ++k)
+      acc = __builtin_fmaf(bf2f(route[(t * topk + k) * hidden + d]), topk_weight[t * topk + k], acc);
+    out[idx] = acc;
+  }
+}
+
+// out = bf16( routed*scale + f(bf16(f(hidden) + f(projected))) )
+template <bool kRoutedBf16>
+__global__ void residual_add_scaled_kernel(const uint16_t* __restrict__ hidden,
+                                           const uint16_t* __restrict__ projected,
+                                           const void* __restrict__ routed, float scale,
+                                           uint16_t* __restrict__ out, long long n) {
+  for (long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<long long>(gridDim.x) * blockDim.x) {
+    const uint16_t rounded = f2bf(bf2f(hidden[i]) + bf2f(projected[i]));
+    const float r = kRoutedBf16 ? bf2f(static_cast<const uint16_t*>(routed)[i])
+                                : static_cast<const float*>(routed)[i];
+    const float scaled = __fmul_rn(r, scale);
+    out[i] = f2bf(__fadd_rn(scaled, bf2f(rounded)));
+  }
+}
+
+__global__ void add_f32_bf16_kernel(const float* __restrict__ a, const uint16_t* __restrict__ b,
+                                    uint16_t* __restrict__ out, long long n) {
+  for (long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<long long>(gridDim.x) * blockDim.x)
+    out[i] = f2bf(__fadd_rn(a[i], bf2f(b[i])));
+}
+
+constexpr int kThreads = 256;
+
+unsigned grid_cap(long long work, int cap) {
+  long long g = (work + kThreads - 1) / kThreads;
+  if (g < 1) g = 1;
+  if (g > cap) g = cap;
+  return static_cast<unsigned>(g);
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int launch_swiglu(const uint16_t* w13, uint16_t* out, int rows, const int32_t* rows_ptr,
+                  int inter, int grid_limit, hipStream_t stream) {
+  const bool vec = inter % 8 == 0 && aligned16(w13) && aligned16(out);
+  const long long work = static_cast<long long>(rows) * (vec ? inter / 8 : inter);
+  const unsigned grid = grid_cap(work, grid_limit);
+  if (vec)
+    hipLaunchKernelGGL(swiglu_vec_kernel, dim3(grid), dim3(kThreads), 0, stream, w13, out, rows,
+                       rows_ptr, inter);
+  else
+    hipLaunchKernelGGL(swiglu_scalar_kernel, dim3(grid), dim3(kThreads), 0, stream, w13, out,
+                       rows, rows_ptr, inter);
+  return launch_status("w13_swiglu");
+}
+
+}  // namespace
+}  // namespace pega
+
+using namespace pega;
+
+// Reference: pegainfer-kernels/src/ffi/kimi.rs:113-119.
+PEGA_API int kimi_marlin_w13_swiglu_cuda(const uint16_t* w13, uint16_t* out, int rows,
+                                         int intermediate_dim, hipStream_t stream) {
+  if (!w13 || !out || rows < 0 || intermediate_dim <= 0)
+    return fail(kInvalidValue, "w13_swiglu: bad arguments");
+  if (rows == 0) return kSuccess;
+  return launch_swiglu(w13, out, rows, nullptr, intermediate_dim, 1 << 20, stream);
+}
+
+// Reference: pegainfer-kernels/src/ffi/kimi.rs:121-129 (rows read on device,
+// clamped to max_rows; occupancy-sized grid of cu_count * 8 blocks).
+PEGA_API int kimi_marlin_w13_swiglu_expanded_cuda(const uint16_t* w13, uint16_t* out,
+                                                  const int32_t* num_tokens_post_padded,
+                                                  int max_rows, int intermediate_dim,
+                                                  int sm_count, hipStream_t stream) {
+  if (!w13 || !out || !num_tokens_post_padded || max_rows < 0 || intermediate_dim <= 0)
+    return fail(kInvalidValue, "w13_swiglu_expanded: bad arguments");
+  if (max_rows == 0) return kSuccess;
+  if (sm_count <= 0) sm_count = current_cu_count();
+  if (sm_count <= 0) return fail(kInvalidValue, "w13_swiglu_expanded: no device");
+  return launch_swiglu(w13, out, max_rows, num_tokens_post_padded, intermediate_dim,
+                       sm_count * 8, stream);
+}
+
+// Reference: pegainfer-kernels/src/ffi/kimi.rs:104-111.
+PEGA_API int kimi_marlin_sum_topk_rows_f32_cuda(const uint16_t* route_output, float* out,
+                                                int active_tokens, int topk, int hidden_dim,
+                                                hipStream_t stream) {
+  if (!route_output || !out || active_tokens < 0 || topk <= 0 || hidden_dim <= 0)
+    return fail(kInvalidValue, "sum_topk_rows: bad arguments");
+  if (active_tokens == 0) return kSuccess;
+  const bool vec = hidden_dim % 8 == 0 && aligned16(route_output) && aligned16(out);
+  const long long work = static_cast<long long>(active_tokens) * (vec ? hidden_dim / 8 : hidden_dim);
+  const unsigned grid = grid_cap(work, 1 << 20);
+  if (vec)
+    hipLaunchKernelGGL(sum_topk_vec_kernel, dim3(grid), dim3(kThreads), 0, stream, route_output,
+                       out, active_tokens, topk, hidden_dim);
+  else
+    hipLaunchKernelGGL(sum_topk_scalar_kernel, dim3(grid), dim3(kThreads), 0, stream,
+                       route_output, out, active_tokens, topk, hidden_dim);
+  return launch_status("sum_topk_rows");
+}
+
+// Weighted fp32 combine of routed rows (DeepSeek-V2-Lite accumulate order);
+// no reference counterpart with this signature (the reference accumulates
+// one expert at a time, dsv2_lite_moe.cu:131-155, in the same per-token order).
+PEGA_API int pega_weighted_topk_sum_f32(const uint16_t* route_output, const float* topk_weight,
+                                        float* out, int active_tokens, int topk, int hidden_dim,
+                                        hipStream_t stream) {
+  if (!route_output || !topk_weight || !out || active_tokens < 0 || topk <= 0 || hidden_dim <= 0)
+    return fail(kInvalidValue, "weighted_topk_sum: bad arguments");
+  if (active_tokens == 0) return kSuccess;
+  const unsigned grid = grid_cap(static_cast<long long>(active_tokens) * hidden_dim, 1 << 20);
+  hipLaunchKernelGGL(weighted_topk_sum_kernel, dim3(grid), dim3(kThreads), 0, stream,
+                     route_output, topk_weight, out, active_tokens, topk, hidden_dim);
+  return launch_status("weighted_topk_sum");
+}
+
+// Reference: pegainfer-kernels/src/ffi/kimi.rs:309-317.
+PEGA_API int kimi_residual_add_scaled_f32_cuda(const uint16_t* hidden, const uint16_t* projected,
+                                               const float* routed_f32, float scale, uint16_t* out,
+                                               int n, hipStream_t stream) {
+  if (!hidden || !projected || !routed_f32 || !out || n < 0)
+    return fail(kInvalidValue, "residual_add_scaled_f32: bad arguments");
+  if (n == 0) return kSuccess;
+  hipLaunchKernelGGL(residual_add_scaled_kernel<false>, dim3(grid_cap(n, 1 << 20)),
+                     dim3(kThreads), 0, stream, hidden, projected,
+                     static_cast<const void*>(routed_f32), scale, out, static_cast<long long>(n));
+  return launch_status("residual_add_scaled_f32");
+}
+
+// Reference: pegainfer-kernels/src/ffi/kimi.rs:319-327.
+PEGA_API int kimi_residual_add_scaled_bf16_cuda(const uint16_t* hidden, const uint16_t* projected,
+                                                const uint16_t* routed, float scale,
+                                                uint16_t* out, int n, hipStream_t stream) {
+  if (!hidden || !projected || !routed || !out || n < 0)
+    return fail(kInvalidValue, "residual_add_scaled_bf16: bad arguments");
+  if (n == 0) return kSuccess;
+  hipLaunchKernelGGL(residual_add_scaled_kernel<true>, dim3(grid_cap(n, 1 << 20)),
+                     dim3(kThreads), 0, stream, hidden, projected,
+                     static_cast<const void*>(routed), scale, out, static_cast<long long>(n));
+  return launch_status("residual_add_scaled_bf16");
+}
+
+// Reference: pegainfer-kernels/src/ffi/kimi.rs:9-15.
+PEGA_API int kimi_add_f32_bf16_to_bf16_cuda(const float* a, const uint16_t* b, uint16_t* out,
+                                            int n, hipStream_t stream) {
+  if (!a || !b || !out || n < 0) return fail(kInvalidValue, "add_f32_bf16: bad arguments");
+  if (n == 0) return kSuccess;
+  hipLaunchKernelGGL(add_f32_bf16_kernel, dim3(grid_cap(n, 1 << 20)), dim3(kThreads), 0, stream,
+                     a, b, out, static_cast<long long>(n));
+  return launch_status("add_f32_bf16");
+}

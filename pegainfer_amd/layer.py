@@ -1,0 +1,171 @@
+"""Composite expert-path layers built from the C-ABI ops.
+
+``RoutedExperts.forward`` is the routed-expert sequence of the reference's
+Kimi-K2 decode layer (pegainfer-kimi-k2/src/runner/moe_nccl.rs:152-203):
+permutation -> zero-fill -> W13 grouped GEMM (top_k, no weight) -> SwiGLU ->
+zero-fill -> W2 grouped GEMM (top_k = 1, bf16 routing weight) -> fp32 top-k
+row sum.  With ``combine="weighted"`` the routing weight is applied in the
+fp32 combine instead (DeepSeek-V2-Lite order, pegainfer-deepseek-v2-lite/
+src/runtime/moe.rs:414-539).  Every buffer is allocated in the constructor;
+``forward`` only enqueues kernels on the current stream.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from . import ops
+
+
+def _dev_u8(a: np.ndarray, device) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a).reshape(-1)).to(device)
+
+
+def _dev_bf16(a: np.ndarray, device) -> torch.Tensor:
+    t = torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint16).view(np.int16)).to(device)
+    return t.view(torch.bfloat16)
+
+
+def package_projection(packed: np.ndarray, scales: np.ndarray, device="cuda") -> ops.MarlinInt4Weight:
+    """Upload checkpoint tensors ([E, out, in/2] u8, [E, out, in/32] bf16 bits) and
+    repack them on the GPU into the device layout."""
+    E, out_dim, half_in = packed.shape
+    w = ops.marlin_int4_reorder(_dev_u8(packed, device), _dev_bf16(scales, device), E,
+                                2 * half_in, out_dim)
+    return w
+
+
+def package_w13(gate, up, device="cuda") -> ops.MarlinInt4Weight:
+    """gate/up = (packed, scales) checkpoint pairs -> fused W13 device package."""
+    g = package_projection(*gate, device=device)
+    u = package_projection(*up, device=device)
+    return ops.marlin_int4_fuse_w13(g, u)
+
+
+class RoutedExperts:
+    """One GPU's share of routed experts with preallocated workspaces."""
+
+    def __init__(self, w13: ops.MarlinInt4Weight, w2: ops.MarlinInt4Weight, *, max_tokens: int,
+                 topk: int, block_size: int, global_start: int = 0, device="cuda",
+                 extra_splits: int = 1):
+        self.w13, self.w2 = w13, w2
+        self.E = w13.local_experts
+        self.H = w13.in_dim
+        self.I = w13.out_dim // 2
+        assert w2.in_dim == self.I and w2.out_dim == self.H and w2.local_experts == self.E
+        self.topk, self.block_size, self.global_start = topk, block_size, global_start
+        self.max_tokens = max_tokens
+        self.route_ws = ops.KimiMarlinRouteWorkspace(max_tokens, block_size, device=device,
+                                                     topk=topk, local_experts=self.E)
+        self.gemm_ws = ops.KimiMarlinWna16Workspace(self.route_ws.max_m_blocks,
+                                                    max(2 * self.I, self.H), block_size,
+                                                    device=device, extra_splits=extra_splits)
+        rows = max_tokens * topk
+        bf = dict(dtype=torch.bfloat16, device=device)
+        self.w13_out = torch.zeros(rows, 2 * self.I, **bf)
+        self.act = torch.zeros(rows, self.I, **bf)
+        self.route_out = torch.zeros(rows, self.H, **bf)
+        self.routing = None
+
+    def forward(self, hidden: torch.Tensor, topk_idx: torch.Tensor, topk_w: torch.Tensor,
+                out_f32: torch.Tensor, combine: str = "sum", w13_timer=None) -> torch.Tensor:
+        """`w13_timer` (optional) exposes start()/stop(mark) and is called around
+        the W13 GEMM launch so a caller can time that kernel with stream events."""
+        T = hidden.shape[0]
+        rows = T * self.topk
+        routing = ops.moe_align_block_size(self.route_ws, topk_idx, T, T, self.global_start)
+        self.routing = routing
+        w13_out = self.w13_out[:rows]
+        act = self.act[:rows]
+        route_out = self.route_out[:rows]
+        w13_out.zero_()
+        mark = w13_timer.start() if w13_timer is not None else None
+        ops.wna16_gemm(self.gemm_ws, routing, hidden, self.w13, topk_w, w13_out, top_k=self.topk,
+                       mul_topk_weights=False, size_m=T)
+        if w13_timer is not None:
+            w13_timer.stop(mark)
+        ops.kimi_marlin_w13_swiglu(w13_out, act, rows, self.I)
+        route_out.zero_()
+        weighted_in_gemm = combine == "sum"
+        ops.wna16_gemm(self.gemm_ws, routing, act, self.w2, topk_w, route_out, top_k=1,
+                       mul_topk_weights=weighted_in_gemm, size_m=rows)
+        if weighted_in_gemm:
+            ops.kimi_marlin_sum_topk_rows_f32(route_out, T, out_f32, self.topk, self.H)
+        else:
+            ops.weighted_topk_sum_f32(route_out, topk_w, T, out_f32, self.topk, self.H)
+        return out_f32
+
+
+class DenseW4A16:
+    """y = x . dequant(W)^T for one W4A16 matrix (a one-expert grouped GEMM with
+    static identity routing)."""
+
+    def __init__(self, w: ops.MarlinInt4Weight, *, max_rows: int, device="cuda",
+                 extra_splits: int = 8):
+        assert w.local_experts == 1
+        self.w = w
+        self.max_rows = max_rows
+        self.block_size = 8 if max_rows <= 8 else (16 if max_rows <= 16 else 64)
+        self.route_ws = ops.KimiMarlinRouteWorkspace(max_rows, self.block_size, device=device,
+                                                     topk=1, local_experts=1)
+        self.gemm_ws = ops.KimiMarlinWna16Workspace(self.route_ws.max_m_blocks, w.out_dim,
+                                                    self.block_size, device=device,
+                                                    extra_splits=extra_splits)
+        self.idx = torch.zeros(max_rows, dtype=torch.int32, device=device)
+        self.ones = torch.ones(max_rows, dtype=torch.float32, device=device)
+        self._routed_rows = None
+
+    def route(self, rows: int):
+        self.routing = ops.moe_align_block_size(self.route_ws, self.idx, rows, rows, 0)
+        self._routed_rows = rows
+
+    def forward(self, x: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
+        rows = x.shape[0]
+        if self._routed_rows != rows:
+            self.route(rows)
+        ops.wna16_gemm(self.gemm_ws, self.routing, x, self.w, self.ones, y, top_k=1,
+                       mul_topk_weights=False, size_m=rows)
+        return y
+
+
+class ExpertFFN:
+    """One expert: W13 -> SwiGLU -> W2 (no routing weight), bf16 out."""
+
+    def __init__(self, w13: ops.MarlinInt4Weight, w2: ops.MarlinInt4Weight, *, max_rows: int,
+                 device="cuda", extra_splits: int = 8):
+        self.up = DenseW4A16(w13, max_rows=max_rows, device=device, extra_splits=extra_splits)
+        self.down = DenseW4A16(w2, max_rows=max_rows, device=device, extra_splits=extra_splits)
+        self.I = w13.out_dim // 2
+        bf = dict(dtype=torch.bfloat16, device=device)
+        self.h13 = torch.zeros(max_rows, w13.out_dim, **bf)
+        self.act = torch.zeros(max_rows, self.I, **bf)
+
+    def forward(self, x: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
+        rows = x.shape[0]
+        self.up.forward(x, self.h13[:rows])
+        ops.kimi_marlin_w13_swiglu(self.h13[:rows], self.act[:rows], rows, self.I)
+        self.down.forward(self.act[:rows], y)
+        return y
+
+
+class Dsv2MoeLayer:
+    """DeepSeek-V2-Lite-shaped MoE: softmax top-k routed experts (weights applied
+    in the fp32 combine, route order = expert id) plus a shared expert, joined
+    as bf16(routed_f32 + shared) (kimi_add_f32_bf16_to_bf16 rounding)."""
+
+    def __init__(self, routed: RoutedExperts, shared: ExpertFFN, device="cuda"):
+        self.routed, self.shared = routed, shared
+        T, H = routed.max_tokens, routed.H
+        self.topk_w = torch.zeros(T, routed.topk, dtype=torch.float32, device=device)
+        self.topk_idx = torch.zeros(T, routed.topk, dtype=torch.int32, device=device)
+        self.routed_f32 = torch.zeros(T, H, dtype=torch.float32, device=device)
+        self.shared_out = torch.zeros(T, H, dtype=torch.bfloat16, device=device)
+
+    def forward(self, hidden: torch.Tensor, logits: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+        T = hidden.shape[0]
+        ops.dsv2_router_select(logits, self.topk_w[:T], self.topk_idx[:T], T, self.routed.topk)
+        self.routed.forward(hidden, self.topk_idx[:T], self.topk_w[:T], self.routed_f32[:T],
+                            combine="weighted")
+        self.shared.forward(hidden, self.shared_out[:T])
+        ops.kimi_add_f32_bf16_to_bf16(self.routed_f32[:T], self.shared_out[:T], out)
+        return out

@@ -1,0 +1,82 @@
+"""GPU parity of the elementwise stages (K3 SwiGLU, K3' expanded SwiGLU, K4
+top-k sum, K8 residual joins, K10 add, DeepSeek-V2-Lite weighted combine):
+bit-exact with the oracle, which restates the reference's rounding points."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_helpers import dev, host
+
+pytestmark = pytest.mark.gpu
+
+
+def _bf16_rand(g, shape, scale=1.0):
+    from oracle import oracle
+    return oracle.f32_to_bf16((g.standard_normal(shape) * scale).astype(np.float32))
+
+
+@pytest.mark.parametrize("rows,inter", [(1, 2048), (512, 2048), (37, 1408), (5, 100)])
+def test_swiglu_bit_exact(oracle, rows, inter):
+    from pegainfer_amd import ops
+    g = np.random.default_rng(rows + inter)
+    w13 = _bf16_rand(g, (rows, 2 * inter), 3.0)
+    w13[0, :3] = [0, 0x8000, 0x7F80]  # +0, -0, +inf gate
+    out = torch.zeros(rows, inter, dtype=torch.bfloat16, device="cuda")
+    ops.kimi_marlin_w13_swiglu(dev(w13), out, rows, inter)
+    ref = oracle.swiglu(w13, inter)
+    got = host(out)
+    fin = np.isfinite((ref.astype(np.uint32) << 16).view(np.float32))
+    assert np.array_equal(got[fin], ref[fin])
+
+
+def test_swiglu_expanded_reads_rows_on_device(oracle):
+    from pegainfer_amd import ops
+    g = np.random.default_rng(9)
+    max_rows, inter = 300, 2048
+    w13 = _bf16_rand(g, (max_rows, 2 * inter))
+    for live in (0, 17, 300, 1000):  # 1000 is clamped to max_rows
+        out = torch.full((max_rows, inter), 3.0, dtype=torch.bfloat16, device="cuda")
+        ops.kimi_marlin_w13_swiglu_expanded(dev(w13), dev(np.array([live], np.int32)), out,
+                                            max_rows, inter)
+        got = host(out)
+        n = min(live, max_rows)
+        if n:
+            assert np.array_equal(got[:n], oracle.swiglu(w13[:n], inter))
+        assert (got[n:] == 0x4040).all()  # untouched rows keep bf16(3.0)
+
+
+@pytest.mark.parametrize("T,topk,H", [(1, 8, 7168), (64, 8, 7168), (3, 6, 2048), (2, 8, 100)])
+def test_sum_topk_rows_bit_exact(oracle, T, topk, H):
+    from pegainfer_amd import ops
+    g = np.random.default_rng(T * H)
+    r = _bf16_rand(g, (T * topk, H), 50.0)
+    out = torch.zeros(T, H, dtype=torch.float32, device="cuda")
+    ops.kimi_marlin_sum_topk_rows_f32(dev(r), T, out, topk, H)
+    assert np.array_equal(host(out), oracle.sum_topk_rows(r, T, topk, H))
+
+
+def test_weighted_topk_sum_bit_exact(oracle):
+    from pegainfer_amd import ops
+    g = np.random.default_rng(2)
+    T, topk, H = 512, 6, 2048
+    r = _bf16_rand(g, (T * topk, H))
+    w = g.random((T, topk)).astype(np.float32)
+    out = torch.zeros(T, H, dtype=torch.float32, device="cuda")
+    ops.weighted_topk_sum_f32(dev(r), dev(w), T, out, topk, H)
+    assert np.array_equal(host(out), oracle.weighted_topk_sum(r, w, T, topk, H))
+
+
+def test_residual_joins_bit_exact(oracle):
+    from pegainfer_amd import ops
+    g = np.random.default_rng(3)
+    n = 64 * 7168
+    h, p = _bf16_rand(g, n), _bf16_rand(g, n)
+    rf = g.standard_normal(n).astype(np.float32)
+    rb = _bf16_rand(g, n)
+    out = torch.zeros(n, dtype=torch.bfloat16, device="cuda")
+    ops.kimi_residual_add_scaled_f32(dev(h), dev(p), dev(rf), 2.827, out)
+    assert np.array_equal(host(out), oracle.residual_add_scaled_f32(h, p, rf, 2.827))
+    ops.kimi_residual_add_scaled_bf16(dev(h), dev(p), dev(rb), 2.827, out)
+    assert np.array_equal(host(out), oracle.residual_add_scaled_bf16(h, p, rb, 2.827))
+    ops.kimi_add_f32_bf16_to_bf16(dev(rf), dev(h), out)
+    assert np.array_equal(host(out), oracle.add_f32_bf16(rf, h))

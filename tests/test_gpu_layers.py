@@ -1,0 +1,209 @@
+"""GPU parity of whole expert-path configurations at BASELINE sizes (C1-C5).
+
+Each layer is checked stage by stage -- every GPU stage against the oracle
+applied to the GPU's own input to that stage, so errors cannot hide behind
+compounding -- and end to end against the oracle's composite, all within
+|gpu - ref| <= 1e-3 + 1e-2 |ref| (indices and permutations bit-exact).  The
+4096-token prefill (C5) is checked on a sample of m-blocks (all rows of the
+largest expert's first and last blocks plus random blocks) and through
+size-independent properties on the rest.
+"""
+import numpy as np
+import pytest
+import torch
+
+from gpu_helpers import assert_bf16_close, assert_f32_close, dev, host
+
+pytestmark = pytest.mark.gpu
+
+
+def _routing_host(r):
+    return {"sorted_token_ids": host(r.sorted_token_ids), "expert_ids": host(r.expert_ids),
+            "num_tokens_post_padded": host(r.num_tokens_post_padded)}
+
+
+def _kimi_weights(cfg_index, E, H, I):
+    from pegainfer_amd import synth
+    g = synth.rng(cfg_index, 1)
+    gate = synth.int4_checkpoint(g, E, I, H)
+    up = synth.int4_checkpoint(g, E, I, H)
+    down = synth.int4_checkpoint(g, E, H, I)
+    return gate, up, down
+
+
+def _routed_layer(gate, up, down, *, tokens, topk, block_size, global_start=0):
+    from pegainfer_amd import layer
+    w13 = layer.package_w13(gate, up)
+    w2 = layer.package_projection(*down)
+    return layer.RoutedExperts(w13, w2, max_tokens=tokens, topk=topk, block_size=block_size,
+                               global_start=global_start)
+
+
+def test_c1_dense_gemv(oracle):
+    from pegainfer_amd import layer, synth
+    g = synth.rng(1, 1)
+    packed, scales = synth.int4_checkpoint(g, 1, 9728, 2560)
+    x = synth.normal_bf16(synth.rng(1, 2), (1, 2560))
+    dense = layer.DenseW4A16(layer.package_projection(packed, scales), max_rows=1)
+    y = torch.zeros(1, 9728, dtype=torch.bfloat16, device="cuda")
+    dense.forward(dev(x), y)
+    routing = _routing_host(dense.routing)
+    ref = oracle.wna16_gemm(x, packed, scales, routing, np.ones(1, np.float32), moe_block_size=8,
+                            top_k=1, mul_topk_weights=False, size_m=1, size_n=9728, size_k=2560)
+    assert_bf16_close(host(y), ref, what="C1")
+
+
+@pytest.mark.parametrize("b", [1, 4, 8])
+def test_c2_expert_ffn(oracle, b):
+    from pegainfer_amd import layer, synth
+    gate, up, down = _kimi_weights(2, 1, 7168, 2048)
+    ffn = layer.ExpertFFN(layer.package_w13(gate, up), layer.package_projection(*down), max_rows=8)
+    x = synth.normal_bf16(synth.rng(2, 2), (b, 7168))
+    y = torch.zeros(b, 7168, dtype=torch.bfloat16, device="cuda")
+    ffn.forward(dev(x), y)
+    w13p = np.concatenate([gate[0], up[0]], axis=1)
+    w13s = np.concatenate([gate[1], up[1]], axis=1)
+    r_up = _routing_host(ffn.up.routing)
+    h13 = host(ffn.h13[:b])
+    ref13 = oracle.wna16_gemm(x, w13p, w13s, r_up, np.ones(b, np.float32), moe_block_size=8,
+                              top_k=1, mul_topk_weights=False, size_m=b, size_n=4096, size_k=7168,
+                              threads=8)
+    assert_bf16_close(h13, ref13, what="C2 W13")
+    act = host(ffn.act[:b])
+    assert np.array_equal(act, oracle.swiglu(h13, 2048))
+    r_dn = _routing_host(ffn.down.routing)
+    ref2 = oracle.wna16_gemm(act, down[0], down[1], r_dn, np.ones(b, np.float32), moe_block_size=8,
+                             top_k=1, mul_topk_weights=False, size_m=b, size_n=7168, size_k=2048,
+                             threads=8)
+    assert_bf16_close(host(y), ref2, what="C2 W2")
+    # end to end against the oracle's own chain
+    e2e = oracle.wna16_gemm(oracle.swiglu(ref13, 2048), down[0], down[1], r_dn,
+                            np.ones(b, np.float32), moe_block_size=8, top_k=1,
+                            mul_topk_weights=False, size_m=b, size_n=7168, size_k=2048, threads=8)
+    assert_bf16_close(host(y), e2e, rtol=2e-2, atol=2e-3, what="C2 end to end")
+
+
+def test_c3_kimi_decode_layer(oracle):
+    from pegainfer_amd import ops, synth
+    E, H, I, T = 48, 7168, 2048, 64
+    gate, up, down = _kimi_weights(3, E, H, I)
+    hidden = synth.normal_bf16(synth.rng(3, 2), (T, H))
+    logits = synth.rng(3, 3).standard_normal((T, 384), dtype=np.float32)
+    bias = np.zeros(384, np.float32)
+    bs = ops.kimi_marlin_block_size(T)
+    assert bs == 16
+    moe = _routed_layer(gate, up, down, tokens=T, topk=8, block_size=bs)
+    w = torch.zeros(T, 8, dtype=torch.float32, device="cuda")
+    idx = torch.zeros(T, 8, dtype=torch.int32, device="cuda")
+    ops.kimi_router_select(dev(logits), dev(bias), w, idx, T)
+    ref_idx, ref_w = oracle.kimi_router(logits, bias, 8, 1.0)
+    assert np.array_equal(host(idx), ref_idx) and np.array_equal(host(w), ref_w)
+    out = torch.zeros(T, H, dtype=torch.float32, device="cuda")
+    moe.forward(dev(hidden), idx, w, out)
+
+    routing = _routing_host(moe.routing)
+    ref_r = oracle.align_block_size(ref_idx.reshape(-1), 0, E, bs)
+    assert np.array_equal(routing["sorted_token_ids"], ref_r["sorted_token_ids"])
+    w13p = np.concatenate([gate[0], up[0]], axis=1)
+    w13s = np.concatenate([gate[1], up[1]], axis=1)
+    g13 = host(moe.w13_out[:T * 8])
+    ref13 = oracle.wna16_gemm(hidden, w13p, w13s, routing, ref_w, moe_block_size=bs, top_k=8,
+                              mul_topk_weights=False, size_m=T, size_n=2 * I, size_k=H, threads=16)
+    assert_bf16_close(g13, ref13, what="C3 W13")
+    act = host(moe.act[:T * 8])
+    assert np.array_equal(act, oracle.swiglu(g13, I))
+    ro = host(moe.route_out[:T * 8])
+    ref2 = oracle.wna16_gemm(act, down[0], down[1], routing, ref_w, moe_block_size=bs, top_k=1,
+                             mul_topk_weights=True, size_m=T * 8, size_n=H, size_k=I, threads=16)
+    assert_bf16_close(ro, ref2, what="C3 W2")
+    got = host(out)
+    assert np.array_equal(got, oracle.sum_topk_rows(ro, T, 8, H))
+    ref_out, _ = oracle.kimi_moe_layer(hidden, w13p, w13s, down[0], down[1], ref_idx.reshape(-1),
+                                       ref_w, global_start=0, local_experts=E, block_size=bs,
+                                       hidden=H, inter=I, threads=16)
+    assert_f32_close(got, ref_out, rtol=2e-2, atol=2e-3, what="C3 end to end")
+
+
+def test_c4_dsv2_layer(oracle):
+    from pegainfer_amd import layer, ops, synth
+    E, H, I, T, topk = 64, 2048, 1408, 512, 6
+    g = synth.rng(4, 1)
+    gate, up, down = (synth.int4_checkpoint(g, E, I, H), synth.int4_checkpoint(g, E, I, H),
+                      synth.int4_checkpoint(g, E, H, I))
+    sg, su, sd = (synth.int4_checkpoint(g, 1, 2 * I, H), synth.int4_checkpoint(g, 1, 2 * I, H),
+                  synth.int4_checkpoint(g, 1, H, 2 * I))
+    hidden = synth.normal_bf16(synth.rng(4, 2), (T, H))
+    logits = synth.rng(4, 3).standard_normal((T, E), dtype=np.float32)
+    bs = ops.kimi_marlin_block_size(T, topk=topk, local_experts=E)
+    routed = _routed_layer(gate, up, down, tokens=T, topk=topk, block_size=bs)
+    shared = layer.ExpertFFN(layer.package_w13(sg, su), layer.package_projection(*sd), max_rows=T)
+    moe = layer.Dsv2MoeLayer(routed, shared)
+    out = torch.zeros(T, H, dtype=torch.bfloat16, device="cuda")
+    moe.forward(dev(hidden), dev(logits), out)
+
+    ref_idx, ref_w = oracle.dsv2_router(logits, topk)
+    assert np.array_equal(host(moe.topk_idx), ref_idx) and np.array_equal(host(moe.topk_w), ref_w)
+    routing = _routing_host(routed.routing)
+    w13p = np.concatenate([gate[0], up[0]], axis=1)
+    w13s = np.concatenate([gate[1], up[1]], axis=1)
+    g13 = host(routed.w13_out[:T * topk])
+    ref13 = oracle.wna16_gemm(hidden, w13p, w13s, routing, ref_w, moe_block_size=bs, top_k=topk,
+                              mul_topk_weights=False, size_m=T, size_n=2 * I, size_k=H, threads=16)
+    assert_bf16_close(g13, ref13, what="C4 W13")
+    act = host(routed.act[:T * topk])
+    assert np.array_equal(act, oracle.swiglu(g13, I))
+    ro = host(routed.route_out[:T * topk])
+    ref2 = oracle.wna16_gemm(act, down[0], down[1], routing, ref_w, moe_block_size=bs, top_k=1,
+                             mul_topk_weights=False, size_m=T * topk, size_n=H, size_k=I,
+                             threads=16)
+    assert_bf16_close(ro, ref2, what="C4 W2")
+    routed_f32 = host(moe.routed_f32)
+    assert np.array_equal(routed_f32, oracle.weighted_topk_sum(ro, ref_w, T, topk, H))
+    sh = host(moe.shared_out)
+    assert np.array_equal(host(out), oracle.add_f32_bf16(routed_f32, sh))
+
+
+def test_c5_kimi_prefill_sampled(oracle):
+    from pegainfer_amd import ops, synth
+    E, H, I, T = 48, 7168, 2048, 4096
+    gate, up, down = _kimi_weights(5, E, H, I)
+    hidden = synth.normal_bf16(synth.rng(5, 2), (T, H))
+    idx, w = synth.zipf_local_topk(synth.rng(5, 3), T)
+    bs = ops.kimi_marlin_block_size(T)
+    moe = _routed_layer(gate, up, down, tokens=T, topk=8, block_size=bs)
+    out = torch.zeros(T, H, dtype=torch.float32, device="cuda")
+    moe.forward(dev(hidden), dev(idx), dev(w), out)
+    routing = _routing_host(moe.routing)
+    ref_r = oracle.align_block_size(idx.reshape(-1), 0, E, bs)
+    for k in ("sorted_token_ids", "expert_ids", "num_tokens_post_padded"):
+        assert np.array_equal(routing[k], ref_r[k]), k
+
+    nblocks = int(routing["num_tokens_post_padded"][0]) // bs
+    eids = routing["expert_ids"][:nblocks]
+    big = np.bincount(eids).argmax()
+    big_blocks = np.flatnonzero(eids == big)
+    g = np.random.default_rng(0)
+    sample = sorted(set([big_blocks[0], big_blocks[-1]] + list(g.choice(nblocks, 6, replace=False))))
+    masked = dict(routing)
+    masked["expert_ids"] = np.where(np.isin(np.arange(routing["expert_ids"].size), sample),
+                                    routing["expert_ids"], -1).astype(np.int32)
+    rows = np.concatenate([routing["sorted_token_ids"][b * bs:(b + 1) * bs] for b in sample])
+    rows = rows[rows < T * 8]
+    w13p = np.concatenate([gate[0], up[0]], axis=1)
+    w13s = np.concatenate([gate[1], up[1]], axis=1)
+    g13 = host(moe.w13_out[:T * 8])
+    ref13 = oracle.wna16_gemm(hidden, w13p, w13s, masked, w, moe_block_size=bs, top_k=8,
+                              mul_topk_weights=False, size_m=T, size_n=2 * I, size_k=H, threads=16)
+    assert_bf16_close(g13[rows], ref13[rows], what="C5 W13 sampled blocks")
+    act = host(moe.act[:T * 8])
+    assert np.array_equal(act[rows], oracle.swiglu(g13[rows], I))
+    ro = host(moe.route_out[:T * 8])
+    ref2 = oracle.wna16_gemm(act, down[0], down[1], masked, w, moe_block_size=bs, top_k=1,
+                             mul_topk_weights=True, size_m=T * 8, size_n=H, size_k=I, threads=16)
+    assert_bf16_close(ro[rows], ref2[rows], what="C5 W2 sampled blocks")
+    # properties on every row: non-local routes stay zero; the combine is the
+    # exact fp32 sum of the routed rows
+    local = (idx.reshape(-1) < E)
+    assert (ro[~local] == 0).all() and (g13[~local] == 0).all()
+    assert (np.abs((ro[local].astype(np.uint32) << 16).view(np.float32)).sum(axis=1) > 0).all()
+    assert np.array_equal(host(out), oracle.sum_topk_rows(ro, T, 8, H))

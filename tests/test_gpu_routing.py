@@ -1,0 +1,136 @@
+"""GPU parity: token -> expert permutation (K1), DeepEP routing metadata (K9)
+and the router select stages, bit-exact against the oracle and the
+reference's known-answer vector."""
+import numpy as np
+import pytest
+import torch
+
+from conftest import load_golden
+from gpu_helpers import dev, host
+
+pytestmark = pytest.mark.gpu
+
+
+def _gpu_align(topk_idx, tokens, topk, global_start, E, bs, kimi=True):
+    from pegainfer_amd import ops
+    ws = ops.KimiMarlinRouteWorkspace(tokens, bs, topk=topk, local_experts=E)
+    # poison the outputs so that untouched slots are visible
+    for t in (ws.sorted_token_ids, ws.expert_ids, ws.expert_offsets, ws.expert_cursor):
+        t.fill_(-7)
+    routing = ops.moe_align_block_size(ws, dev(np.ascontiguousarray(topk_idx, np.int32).reshape(-1)),
+                                       tokens, tokens, global_start)
+    return ws, routing
+
+
+def _check_against_oracle(oracle, ws, topk_idx, global_start, E, bs):
+    ref = oracle.align_block_size(np.asarray(topk_idx, np.int32).reshape(-1), global_start, E, bs,
+                                  ws.max_padded_tokens, ws.max_m_blocks)
+    assert np.array_equal(host(ws.sorted_token_ids), ref["sorted_token_ids"])
+    assert np.array_equal(host(ws.expert_ids), ref["expert_ids"])
+    assert np.array_equal(host(ws.num_tokens_post_padded), ref["num_tokens_post_padded"])
+    assert np.array_equal(host(ws.expert_offsets).view(np.uint32), ref["expert_offsets"])
+    assert np.array_equal(host(ws.expert_cursor).view(np.uint32), ref["expert_cursor"])
+
+
+def test_align_reference_kat():
+    g = load_golden("align_kat.npz")
+    ws, routing = _gpu_align(g["topk_idx"], int(g["active_tokens"]), 8, int(g["global_start"]),
+                             48, int(g["block_size"]))
+    total = int(host(ws.num_tokens_post_padded)[0])
+    assert total == g["expected_sorted"].size and total % 8 == 0
+    assert np.array_equal(host(ws.sorted_token_ids)[:total], g["expected_sorted"])
+    n = g["expected_expert_ids"].size
+    assert np.array_equal(host(ws.expert_ids)[:n], g["expected_expert_ids"])
+    assert routing.manifest_attrs()["sentinel_token_id"] == "56"
+
+
+@pytest.mark.parametrize("tokens,bs,seed", [(1, 8, 0), (7, 8, 1), (64, 16, 2), (200, 32, 3),
+                                            (300, 48, 4), (4096, 64, 5), (16384, 64, 6)])
+def test_align_random_vs_oracle(oracle, tokens, bs, seed):
+    g = np.random.default_rng(seed)
+    gs = int(g.integers(0, 337))
+    idx = g.integers(0, 384, size=(tokens, 8)).astype(np.int32)
+    ws, _ = _gpu_align(idx, tokens, 8, gs, 48, bs)
+    _check_against_oracle(oracle, ws, idx, gs, 48, bs)
+
+
+def test_align_zipf_prefill_vs_oracle(oracle):
+    from pegainfer_amd import synth
+    idx, _ = synth.zipf_local_topk(synth.rng(5, 0), 4096)
+    ws, _ = _gpu_align(idx, 4096, 8, 0, 48, 64)
+    _check_against_oracle(oracle, ws, idx, 0, 48, 64)
+
+
+def test_align_edge_cases(oracle):
+    # no local routes at all
+    idx = np.full((5, 8), 300, np.int32)
+    ws, _ = _gpu_align(idx, 5, 8, 0, 48, 16)
+    assert int(host(ws.num_tokens_post_padded)[0]) == 0
+    assert (host(ws.sorted_token_ids) == 40).all() and (host(ws.expert_ids) == -1).all()
+    _check_against_oracle(oracle, ws, idx, 0, 48, 16)
+    # every route to one expert (maximum segment)
+    idx = np.full((500, 8), 17, np.int32)
+    ws, _ = _gpu_align(idx, 500, 8, 0, 48, 64)
+    _check_against_oracle(oracle, ws, idx, 0, 48, 64)
+    # capacity exactly at the bound routes + E*(bs-1)
+    idx = np.arange(48 * 8, dtype=np.int32).reshape(48, 8) % 48
+    ws, _ = _gpu_align(idx, 48, 8, 0, 48, 16)
+    _check_against_oracle(oracle, ws, idx, 0, 48, 16)
+
+
+@pytest.mark.parametrize("E,topk,tokens,bs", [(64, 6, 512, 64), (1, 1, 8, 8), (1, 1, 513, 64),
+                                              (224, 8, 100, 16)])
+def test_align_general_shapes(oracle, E, topk, tokens, bs):
+    g = np.random.default_rng(E + topk)
+    idx = g.integers(0, max(E, 2), size=(tokens, topk)).astype(np.int32)
+    ws, _ = _gpu_align(idx, tokens, topk, 0, E, bs)
+    _check_against_oracle(oracle, ws, idx, 0, E, bs)
+
+
+def test_deepep_routing_vs_oracle(oracle):
+    from pegainfer_amd import ops
+    g = np.random.default_rng(3)
+    E, align, bs = 48, 16, 16
+    psum, cur = [], 0
+    for c in g.integers(0, 40, size=E):
+        cur = -(-cur // align) * align + int(c)
+        psum.append(cur)
+    psum.append(-(-cur // align) * align)
+    ws = ops.KimiMarlinRouteWorkspace(512, bs)
+    cap = psum[-1] + 64
+    ops.kimi_deepep_build_marlin_routing_on_stream(ws, dev(np.array(psum, np.int32)), align, cap)
+    ref = oracle.deepep_build_routing(np.array(psum, np.int32), E, align, bs, cap, -(-cap // bs))
+    assert np.array_equal(host(ws.sorted_token_ids)[:cap], ref["sorted_token_ids"])
+    assert np.array_equal(host(ws.expert_ids)[:-(-cap // bs)], ref["expert_ids"])
+    assert int(host(ws.num_tokens_post_padded)[0]) == psum[-1]
+
+
+@pytest.mark.parametrize("tokens,seed", [(1, 0), (64, 1), (4096, 2)])
+def test_kimi_router_select_bit_exact(oracle, tokens, seed):
+    from pegainfer_amd import ops
+    g = np.random.default_rng(seed)
+    logits = g.standard_normal((tokens, 384)).astype(np.float32)
+    bias = (g.standard_normal(384) * 0.05).astype(np.float32) if seed else np.zeros(384, np.float32)
+    w = torch.zeros(tokens, 8, dtype=torch.float32, device="cuda")
+    idx = torch.zeros(tokens, 8, dtype=torch.int32, device="cuda")
+    ops.kimi_router_select(dev(logits), dev(bias), w, idx, tokens)
+    ref_idx, ref_w = oracle.kimi_router(logits, bias, 8, 1.0)
+    assert np.array_equal(host(idx), ref_idx)
+    assert np.array_equal(host(w), ref_w)
+
+
+@pytest.mark.parametrize("tokens,seed", [(1, 0), (512, 1)])
+def test_dsv2_router_select_bit_exact(oracle, tokens, seed):
+    from pegainfer_amd import ops
+    g = np.random.default_rng(seed)
+    logits = g.standard_normal((tokens, 64)).astype(np.float32)
+    if tokens > 1:
+        logits[0] = load_golden("misc_kat.npz")["dsv2_logits"]
+    w = torch.zeros(tokens, 6, dtype=torch.float32, device="cuda")
+    idx = torch.zeros(tokens, 6, dtype=torch.int32, device="cuda")
+    ops.dsv2_router_select(dev(logits), w, idx, tokens, 6)
+    ref_idx, ref_w = oracle.dsv2_router(logits, 6)
+    assert np.array_equal(host(idx), ref_idx)
+    assert np.array_equal(host(w), ref_w)
+    if tokens > 1:
+        assert list(host(idx)[0]) == [7, 10, 20, 41, 54, 58]

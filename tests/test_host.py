@@ -1,0 +1,164 @@
+"""Host-side checks that need no GPU: the C-ABI library loads and exports every
+symbol include/pega_moe.h declares, argument validation rejects bad shapes
+before any launch (the reference's guards), and the Python mirror's shape
+logic matches the reference's CPU unit tests
+(pegainfer-kernels/src/ops/kimi_k2/experts.rs:1512-1641,
+pegainfer-kimi-k2/src/runner/worker/runtime.rs:99-109)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "pega_moe.h")
+
+
+def _declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\*?(\w+)\(", text, flags=re.M)))
+
+
+def test_header_declares_the_reference_entry_points():
+    syms = _declared_symbols()
+    for name in ["kimi_moe_marlin_align_block_size_cuda", "kimi_marlin_wna16_gemm_cuda",
+                 "kimi_marlin_w13_swiglu_cuda", "kimi_marlin_w13_swiglu_expanded_cuda",
+                 "kimi_marlin_sum_topk_rows_f32_cuda", "kimi_marlin_int4_reorder_weight_cuda",
+                 "kimi_marlin_int4_reorder_scale_cuda", "kimi_marlin_int4_fuse_w13_cuda",
+                 "kimi_residual_add_scaled_f32_cuda", "kimi_residual_add_scaled_bf16_cuda",
+                 "kimi_add_f32_bf16_to_bf16_cuda", "kimi_deepep_build_marlin_routing_on_stream",
+                 "pegainfer_kernels_last_error"]:
+        assert name in syms, name
+
+
+def test_library_exports_every_declared_symbol():
+    from pegainfer_amd import _lib
+    L = _lib.lib()
+    syms = _declared_symbols()
+    assert len(syms) >= 20
+    for name in syms:
+        assert hasattr(L, name), f"{name} declared in pega_moe.h but not exported"
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+
+
+def _call(name, *args):
+    from pegainfer_amd import _lib
+    return getattr(_lib.lib(), name)(*args), _lib.last_error()
+
+
+NULL = None
+FAKE = ctypes.c_void_p(0x1000)  # never dereferenced: validation rejects first
+
+
+def test_align_rejects_reference_invalid_shapes():
+    args = [FAKE] * 6
+    # topk != 8 (kimi_experts.cu:217)
+    rc, msg = _call("kimi_moe_marlin_align_block_size_cuda", *args, 7, 7, 96, 48, 8, 400, 50, NULL)
+    assert rc == 1 and "topk" in msg
+    # local_experts != 48
+    rc, _ = _call("kimi_moe_marlin_align_block_size_cuda", *args, 7, 8, 96, 47, 8, 400, 50, NULL)
+    assert rc == 1
+    # block size 24 not allowed (:221)
+    rc, msg = _call("kimi_moe_marlin_align_block_size_cuda", *args, 7, 8, 96, 48, 24, 400, 50, NULL)
+    assert rc == 1 and "block_size" in msg
+    # capacity below routes + E*(bs-1) = 56 + 336 = 392 (:224-229)
+    rc, msg = _call("kimi_moe_marlin_align_block_size_cuda", *args, 7, 8, 96, 48, 8, 391, 49, NULL)
+    assert rc == 1 and "capacity" in msg
+    # null pointer
+    rc, _ = _call("kimi_moe_marlin_align_block_size_cuda", NULL, *args[1:], 7, 8, 96, 48, 8, 392, 49, NULL)
+    assert rc == 1
+    # zero tokens
+    rc, _ = _call("kimi_moe_marlin_align_block_size_cuda", *args, 0, 8, 96, 48, 8, 392, 49, NULL)
+    assert rc == 1
+
+
+def test_gemm_rejects_reference_invalid_shapes():
+    from pegainfer_amd import _lib
+    f = _lib.lib().kimi_marlin_wna16_gemm_cuda
+
+    def call(**kw):
+        base = dict(workspace_len=4096, sorted_len=1232, bs=16, top_k=8, mul=False, m=64, n=4096,
+                    k=7168, experts=48, group=32)
+        base.update(kw)
+        return f(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, base["workspace_len"],
+                 base["sorted_len"], base["bs"], base["top_k"], base["mul"], base["m"], base["n"],
+                 base["k"], base["experts"], base["group"], 0, NULL)
+
+    assert call(experts=47) == 1
+    assert call(group=64) == 1
+    assert call(bs=24) == 1
+    assert call(n=4000) == 1
+    assert call(k=7160) == 1
+    assert call(m=0) == 1
+    rc = f(FAKE, FAKE, NULL, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4096, 1232, 16, 8, False, 64,
+           4096, 7168, 48, 32, 0, NULL)
+    assert rc == 1  # c_tmp required (kimi_marlin_wna16.cu:272-274)
+
+
+def test_repack_and_elementwise_reject_bad_arguments():
+    assert _call("kimi_marlin_int4_reorder_weight_cuda", FAKE, FAKE, 64, 64, 47, 32, NULL)[0] == 1
+    assert _call("kimi_marlin_int4_reorder_weight_cuda", FAKE, FAKE, 64, 60, 48, 32, NULL)[0] == 1
+    assert _call("kimi_marlin_int4_reorder_scale_cuda", FAKE, FAKE, 64, 64, 48, 16, NULL)[0] == 1
+    assert _call("kimi_marlin_int4_fuse_w13_cuda", *([FAKE] * 5), NULL, 64, 64, 48, 32, NULL)[0] == 1
+    assert _call("kimi_marlin_w13_swiglu_cuda", FAKE, FAKE, -1, 64, NULL)[0] == 1
+    assert _call("kimi_marlin_w13_swiglu_cuda", FAKE, FAKE, 0, 64, NULL)[0] == 0  # no-op
+    assert _call("kimi_marlin_sum_topk_rows_f32_cuda", FAKE, FAKE, 4, 0, 64, NULL)[0] == 1
+    assert _call("kimi_marlin_sum_topk_rows_f32_cuda", FAKE, FAKE, 0, 8, 64, NULL)[0] == 0
+    assert _call("kimi_residual_add_scaled_f32_cuda", FAKE, FAKE, NULL, ctypes.c_float(2.8), FAKE,
+                 8, NULL)[0] == 1
+    assert _call("kimi_add_f32_bf16_to_bf16_cuda", FAKE, FAKE, FAKE, -1, NULL)[0] == 1
+    assert _call("pega_kimi_router_select", FAKE, FAKE, FAKE, FAKE, 4, 384, 400,
+                 ctypes.c_float(1.0), NULL)[0] == 1
+    assert _call("pega_dsv2_router_select", FAKE, FAKE, FAKE, 4, 64, 0, NULL)[0] == 1
+
+
+# ------------------------------------------------------------- Python mirror logic
+def test_manifest_shapes_match_reference_unit_tests():
+    from pegainfer_amd import ops
+    m = ops.KimiInt4WeightManifest.ep8(ops.KimiInt4ExpertRole.W1Gate, 3,
+                                        ops.KimiInt4NibbleOrder.LowThenHigh)
+    m.validate()
+    assert m.local_experts == 48 and m.local_expert_offset == 144
+    assert m.packed_shape.elements() == 48 * 2048 * (7168 // 2)
+    assert m.scale_shape.elements() == 48 * 2048 * (7168 // 32)
+    d = ops.KimiInt4WeightManifest.ep8(ops.KimiInt4ExpertRole.W2Down, 0,
+                                        ops.KimiInt4NibbleOrder.LowThenHigh)
+    d.validate()
+    assert d.logical_shape == ops.KimiInt4LogicalShape(out_dim=7168, in_dim=2048)
+    assert d.packed_shape.elements() == 48 * 7168 * (2048 // 2)
+    assert d.marlin_packed_u32_elements() * 4 == d.packed_shape.elements()
+    import dataclasses
+    bad = dataclasses.replace(m, group_size=64)
+    with pytest.raises(ValueError):
+        bad.validate()
+    with pytest.raises(ValueError):
+        dataclasses.replace(m, local_experts=47).validate()
+
+
+def test_capacity_and_block_size_policy():
+    from pegainfer_amd import ops
+    cap = ops.marlin_padded_route_capacity(7, 8)
+    assert cap == 7 * 8 + 48 * 7 and -(-cap // 8) == 49
+    # runtime.rs:99-109: smallest bs with T*8/48/bs < 0.9
+    # (T < 5.4 * bs): 8 up to 43 tokens, 16 up to 86, 32 up to 172, 48 up to 259
+    for t, bs in [(1, 8), (43, 8), (44, 16), (64, 16), (86, 16), (87, 32), (172, 32),
+                  (173, 48), (259, 48), (260, 64), (4096, 64)]:
+        assert ops.kimi_marlin_block_size(t) == bs, t
+    with pytest.raises(ValueError):
+        ops.validate_marlin_block_size(24)
+
+
+def test_synth_routing_generators_are_seeded_and_shaped():
+    import numpy as np
+    from pegainfer_amd import synth
+    idx, w = synth.zipf_local_topk(synth.rng(5, 1), 512, routes_target=800)
+    idx2, _ = synth.zipf_local_topk(synth.rng(5, 1), 512, routes_target=800)
+    assert np.array_equal(idx, idx2)
+    assert idx.shape == (512, 8) and np.allclose(w.sum(1), 1.0, atol=1e-6)
+    for row in idx:
+        assert len(set(row.tolist())) == 8
+        assert 1 <= (row < 48).sum() <= 2
+    counts = np.bincount(idx[idx < 48], minlength=48)
+    assert counts.max() > 4 * max(1, np.median(counts))  # skewed
