@@ -43,7 +43,21 @@ def parse():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--only", default="", help="comma list of configs to run (c1..c5)")
+    p.add_argument("--calibrate-copy", action="store_true",
+                   help="only run a plain 256 MiB device copy (reference kernel for the "
+                        "FETCH_SIZE / WRITE_SIZE counter scale) and exit")
     return p.parse_args()
+
+
+def calibrate_copy(torch):
+    n = 256 * 1024 * 1024 // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "copy", "bytes_read": n * 4, "bytes_written": n * 4,
+                      "launches": 5}))
 
 
 class EventTimer:
@@ -270,6 +284,9 @@ def main():
         print(json.dumps({"error": "no GPU visible"}))
         sys.exit(2)
     torch.cuda.set_device(0)
+    if args.calibrate_copy:
+        calibrate_copy(torch)
+        return
     import pegainfer_amd
     pegainfer_amd.load()
     only = set(x.strip() for x in args.only.split(",") if x.strip())

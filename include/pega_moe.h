@@ -102,9 +102,8 @@ int pega_marlin_int4_fuse_w13(const uint8_t* gate_w, const uint8_t* up_w, uint8_
 /* ---------------- grouped W4A16 GEMM ---------------- */
 
 /* Replaces kimi_marlin_wna16_gemm_cuda, pegainfer-kernels/src/ffi/kimi.rs:131-152
- * (csrc/kimi_k2/kimi_marlin_wna16.cu:241-343,414-442).  c_tmp follows the reference's
- * sizing (size_n * sorted_token_ids_len floats, x2 for block size 8); workspace (locks)
- * is left all-zero on return. */
+ * (csrc/kimi_k2/kimi_marlin_wna16.cu:241-343,414-442).  c_tmp and workspace (locks) are
+ * required as in the reference but not accessed: K is split inside each workgroup. */
 int kimi_marlin_wna16_gemm_cuda(const uint16_t* input, uint16_t* output, float* c_tmp,
                                 const uint8_t* b_qweight, const uint16_t* b_scales,
                                 int32_t* workspace, const int32_t* sorted_token_ids,
@@ -115,7 +114,8 @@ int kimi_marlin_wna16_gemm_cuda(const uint16_t* input, uint16_t* output, float* 
                                 int local_experts, int group_size, int sm_count,
                                 hipStream_t stream);
 
-/* No reference counterpart: shape-general form with an explicit c_tmp length (floats). */
+/* No reference counterpart: shape-general form (any expert count; c_tmp / workspace unused
+ * and may be NULL). */
 int pega_wna16_gemm(const uint16_t* input, uint16_t* output, float* c_tmp, long long c_tmp_len,
                     const uint8_t* b_qweight, const uint16_t* b_scales, int32_t* workspace,
                     int workspace_len, const int32_t* sorted_token_ids, const int32_t* expert_ids,

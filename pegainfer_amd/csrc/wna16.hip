@@ -124,7 +124,6 @@ struct GemmArgs {
   const float* topk_w;
   int sorted_len, bs, top_k, mul, size_m, size_n, size_k;
   int num_experts;  // expert ids outside [0, num_experts) are skipped
-  int splits;       // cross-workgroup K splits (decode kernel)
 };
 
 __device__ __forceinline__ uint16_t epilogue_value(float acc, int sid, const GemmArgs& p) {
@@ -133,28 +132,79 @@ __device__ __forceinline__ uint16_t epilogue_value(float acc, int sid, const Gem
   return c;
 }
 
+// Raw buffer resources: base address in SGPRs, 32-bit per-lane offsets, a
+// per-iteration scalar offset, and hardware range checking (reads at or past
+// `bytes` return zero, which is how rows that are not routed here read zeros
+// without a branch).
+typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4_t;
+constexpr uint32_t kOutOfRange = 0x80000000u;  // voffset that fails every range check
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
+                                           static_cast<int>(bytes), 0x00020000);
+}
+// Cache policy of a load: kCached for data other workgroups re-read (the
+// activations), kStream (non-temporal) for bytes read exactly once per launch
+// (the decode path's weights and scales), which then do not evict the rest.
+constexpr int kCached = 0;
+constexpr int kStream = 2;
+
+template <int kPolicy = kCached>
+__device__ __forceinline__ uint32_t buf_load_b32(__amdgpu_buffer_rsrc_t r, uint32_t voff,
+                                                 uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(voff), static_cast<int>(soff),
+                                              kPolicy);
+}
+template <int kPolicy = kCached>
+__device__ __forceinline__ u32x4_t buf_load_b128(__amdgpu_buffer_rsrc_t r, uint32_t voff,
+                                                 uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(voff), static_cast<int>(soff),
+                                               kPolicy);
+}
+
 // ---------------------------------------------------------------------------
-// Decode kernel: one workgroup per (m-block, 64-column tile, K split), WK
-// waves splitting the K range, rows <= 32 (one MFMA row block), activations
-// read straight from global memory (only valid rows are loaded).
+// Decode kernel: one workgroup per (m-block, 64-column tile); WK waves split
+// the K range and are reduced through LDS in a fixed wave order (bit-for-bit
+// reproducible).  The block's rows (<= 32, one MFMA row block) occupy NI
+// accumulator elements per lane (rows < bs).
+//
+// Weight traffic is shaped for the texture-address unit: per quant group a
+// wave issues ONE 16-byte load per lane (lane L takes word row th = L%32 of
+// k-tile 2g + L/32, i.e. both 512-byte tiles contiguously), then transposes
+// through a per-wave LDS slot so that lane (c, h) reads its four fragment
+// words (th = 4*(c%8) + jj, w = c/8) as one 16-byte LDS read.  Slot layout:
+// word (th, w) of tile h at dword h*160 + w*32 + th (the 160 stride puts the
+// two tiles in opposite bank halves: writes and reads are conflict-free).
+// Lanes whose activation row is not routed here read zeros through an
+// out-of-range buffer offset.  D groups per wave are in flight.
 // ---------------------------------------------------------------------------
-template <int WK>
+constexpr int kSlotDwords = 320;
+
+struct GroupRegs {
+  u32x4_t raw;  // 4 words (th, w = 0..3) of this lane's k-tile
+  uint32_t sp;
+  u32x4_t a0, a1;
+};
+
+template <int WK, int NI, int D>
 __global__ __launch_bounds__(64 * WK) void wna16_decode_kernel(GemmArgs p) {
   __shared__ int s_sid[32];
-  __shared__ float s_red[WK][32][64];
-  __shared__ int s_last;
+  __shared__ float s_red[WK][2 * NI][64];
+  __shared__ __align__(16) uint32_t s_w[WK][kSlotDwords];
 
-  const int n_tiles = p.size_n >> 6;
-  const int nt = blockIdx.x % n_tiles;
-  const int split = blockIdx.x / n_tiles;
+  const int nt = blockIdx.x;
   const int mb = blockIdx.y;
   int ntp = p.ntp[0];
   if (ntp > p.sorted_len) ntp = p.sorted_len;
   if (mb >= ntp / p.bs) return;  // whole blocks only: rows stay inside sorted_len
-  const int expert = p.expert_ids[mb];
+  // readfirstlane: values the compiler cannot prove wave-uniform but that are
+  // (block-level loads, wave index) go to SGPRs, so buffer descriptors and
+  // scalar offsets built from them need no per-lane waterfall loops.
+  const int expert = __builtin_amdgcn_readfirstlane(p.expert_ids[mb]);
   if (expert < 0 || expert >= p.num_experts) return;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int valid_limit = p.size_m * p.top_k;
   if (tid < 32) {
     int sid = valid_limit;
@@ -165,141 +215,150 @@ __global__ __launch_bounds__(64 * WK) void wna16_decode_kernel(GemmArgs p) {
 
   const int c = lane & 31, h = lane >> 5;
   const int K = p.size_k, N = p.size_n;
+  const int n_tiles = N >> 6;
   const int groups = K >> 5;
-  const int slices = p.splits * WK;
-  const int slice = split * WK + wave;
-  const int g0 = (groups * slice) / slices, g1 = (groups * (slice + 1)) / slices;
+  const int g0 = (groups * wave) / WK, g1 = (groups * (wave + 1)) / WK;
 
-  // activation row of this lane (row m = c)
+  const uint32_t expert_bytes = static_cast<uint32_t>(N) * static_cast<uint32_t>(K) / 2u;
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(
+      p.qweight + static_cast<long long>(expert) * (expert_bytes / 4u), expert_bytes);
+  const uint32_t tile_row_bytes = static_cast<uint32_t>(n_tiles) * 512u;
+  const uint32_t w_voff = static_cast<uint32_t>(h) * tile_row_bytes +
+                          static_cast<uint32_t>(nt) * 512u + static_cast<uint32_t>(c) * 16u;
+  const uint32_t w_step = 2u * tile_row_bytes;  // bytes per quant group
+  const uint32_t scale_bytes = static_cast<uint32_t>(groups) * static_cast<uint32_t>(N) * 2u;
+  const __amdgpu_buffer_rsrc_t sr = make_rsrc(
+      p.scales + static_cast<long long>(expert) * groups * N, scale_bytes);
+  const uint32_t s_voff = (static_cast<uint32_t>(nt) * 64u + 8u * (c & 7) + 2u * (c >> 3)) * 2u;
+  const uint32_t s_step = static_cast<uint32_t>(N) * 2u;
   const int my_sid = s_sid[c];
-  const bool row_ok = my_sid < valid_limit;
-  const uint16_t* arow = p.input + static_cast<long long>(row_ok ? my_sid / p.top_k : 0) * K;
+  const __amdgpu_buffer_rsrc_t ar =
+      make_rsrc(p.input, static_cast<uint32_t>(p.size_m) * static_cast<uint32_t>(K) * 2u);
+  const uint32_t a_voff =
+      my_sid < valid_limit
+          ? (static_cast<uint32_t>(my_sid / p.top_k) * static_cast<uint32_t>(K) + 16u * h) * 2u
+          : kOutOfRange;
 
-  const long long expert_words = static_cast<long long>(N) * (K >> 3);
-  const uint32_t* wbase = p.qweight + expert * expert_words +
-                          static_cast<long long>(nt) * 128 + 16 * (c & 7) + (c >> 3);
-  const long long tile_row_words = static_cast<long long>(n_tiles) * 128;  // one k-tile row
-  const uint32_t* sbase = reinterpret_cast<const uint32_t*>(
-      p.scales + static_cast<long long>(expert) * (K >> 5) * N + nt * 64 + 8 * (c & 7) +
-      2 * (c >> 3));
-  const int srow_words = N >> 1;
+  uint32_t* slot_w = &s_w[wave][h * 160 + c];          // this lane's write column
+  const uint32_t* slot_r = &s_w[wave][h * 160 + 4 * c];  // this lane's 16-byte read
+
+  auto load_group = [&](GroupRegs& r, int g) {
+    g = min(max(g, 0), groups - 1);  // every scalar offset stays inside the expert
+    r.raw = buf_load_b128<kStream>(wr, w_voff, static_cast<uint32_t>(g) * w_step);
+    r.sp = buf_load_b32<kStream>(sr, s_voff, static_cast<uint32_t>(g) * s_step);
+    // rows not routed here have an out-of-range offset and read zeros; no
+    // branch, so the loads stay in flight across groups
+    r.a0 = buf_load_b128(ar, a_voff, static_cast<uint32_t>(g) * 64u);
+    r.a1 = buf_load_b128(ar, a_voff + 16u, static_cast<uint32_t>(g) * 64u);
+  };
 
   const uint32_t k1024 = 0x64006400u, k64 = 0x54005400u;
   floatx16_t accx = {}, accy = {};
-
-  for (int g = g0; g < g1; ++g) {
-    const uint32_t* wp = wbase + (2LL * g + h) * tile_row_words;
-    uint32_t w[4];
+  GroupRegs slot[D];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) w[j] = wp[4 * j];
-    const uint32_t sp = sbase[static_cast<long long>(g) * srow_words];
-    uint4 a0 = make_uint4(0, 0, 0, 0), a1 = make_uint4(0, 0, 0, 0);
-    if (row_ok) {
-      const uint4* ap = reinterpret_cast<const uint4*>(arow + 32 * g + 16 * h);
-      a0 = ap[0];
-      a1 = ap[1];
-    }
-    const BFrags b = make_b(w, sp, k1024, k64);
-    const bf16x8_t A1 = as_bf16x8(a0.x, a0.y, a1.x, a1.y);
-    const bf16x8_t A2 = as_bf16x8(a0.z, a0.w, a1.z, a1.w);
+  for (int q = 0; q < D; ++q) load_group(slot[q], g0 + q < g1 ? g0 + q : g1 - 1);
+
+  auto compute_group = [&](const GroupRegs& r) {
+    // transpose the tile words into fragment order through this wave's slot
+    slot_w[0] = r.raw[0];
+    slot_w[32] = r.raw[1];
+    slot_w[64] = r.raw[2];
+    slot_w[96] = r.raw[3];
+    const u32x4_t fw = *reinterpret_cast<const u32x4_t*>(slot_r);
+    const uint32_t w4[4] = {fw[0], fw[1], fw[2], fw[3]};
+    const BFrags b = make_b(w4, r.sp, k1024, k64);
+    const bf16x8_t A1 = as_bf16x8(r.a0[0], r.a0[1], r.a1[0], r.a1[1]);
+    const bf16x8_t A2 = as_bf16x8(r.a0[2], r.a0[3], r.a1[2], r.a1[3]);
     accx = mfma(A1, b.x1, accx);
     accx = mfma(A2, b.x2, accx);
     accy = mfma(A1, b.y1, accy);
     accy = mfma(A2, b.y2, accy);
-  }
+  };
 
-  // Deterministic reduction over the WK waves (fixed order 0..WK-1).
+  // Main loop over whole rounds of D groups: no branch inside, so the loads
+  // of the next round stay in flight while this round computes.  The slot a
+  // group came from is refilled with the group D ahead (clamped to the last
+  // group of the slice, fetched again and never used).
+  const int rounds = (g1 - g0) / D;
+  int g = g0;
+  for (int r = 0; r < rounds; ++r, g += D) {
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
+    for (int q = 0; q < D; ++q) {
+      compute_group(slot[q]);
+      load_group(slot[q], min(g + q + D, g1 - 1));
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < D - 1; ++q)
+    if (g + q < g1) compute_group(slot[q]);
+
+  // Deterministic reduction over the WK waves (fixed order 0..WK-1); only the
+  // NI accumulator elements that hold rows < bs are exchanged.
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
     s_red[wave][i][lane] = accx[i];
-    s_red[wave][16 + i][lane] = accy[i];
+    s_red[wave][NI + i][lane] = accy[i];
   }
   __syncthreads();
 
   const int n0 = nt * 64 + (c >> 3) * 16 + (c & 7);
-  // Each wave finalises 32/WK of the lane's 32 values.
-  constexpr int kPer = 32 / WK;
-  float v[kPer];
-#pragma unroll
-  for (int q = 0; q < kPer; ++q) {
-    const int j = wave * kPer + q;
+  for (int j = wave; j < 2 * NI; j += WK) {
     float s = 0.0f;
 #pragma unroll
     for (int w = 0; w < WK; ++w) s += s_red[w][j][lane];
-    v[q] = s;
-  }
-
-  if (p.splits > 1) {
-    // Partial of this split -> c_tmp[split][mb*bs + row][n]; the last of the
-    // splits to arrive sums the partials in split order and writes C.
-    const long long rows_cap = p.sorted_len;
-#pragma unroll
-    for (int q = 0; q < kPer; ++q) {
-      const int j = wave * kPer + q;
-      const int row = acc_row(j & 15, h);
-      const int n = (j < 16) ? n0 : n0 + 8;
-      if (row < p.bs)
-        p.c_tmp[(split * rows_cap + mb * p.bs + row) * N + n] = v[q];
-    }
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-      const int old = atomicAdd(&p.locks[mb * n_tiles + nt], 1);
-      s_last = (old == p.splits - 1);
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-#pragma unroll
-    for (int q = 0; q < kPer; ++q) {
-      const int j = wave * kPer + q;
-      const int row = acc_row(j & 15, h);
-      const int n = (j < 16) ? n0 : n0 + 8;
-      float s = 0.0f;
-      if (row < p.bs)
-        for (int sp = 0; sp < p.splits; ++sp)
-          s += __builtin_nontemporal_load(&p.c_tmp[(sp * rows_cap + mb * p.bs + row) * N + n]);
-      v[q] = s;
-    }
-    if (tid == 0) p.locks[mb * n_tiles + nt] = 0;
-  }
-
-#pragma unroll
-  for (int q = 0; q < kPer; ++q) {
-    const int j = wave * kPer + q;
-    const int row = acc_row(j & 15, h);
-    const int n = (j < 16) ? n0 : n0 + 8;
+    const int row = acc_row(j < NI ? j : j - NI, h);
+    const int n = (j < NI) ? n0 : n0 + 8;
     if (row < p.bs) {
       const int sid = s_sid[row];
       if (sid < valid_limit)
-        p.output[static_cast<long long>(sid) * N + n] = epilogue_value(v[q], sid, p);
+        p.output[static_cast<long long>(sid) * N + n] = epilogue_value(s, sid, p);
     }
   }
+}
+
+constexpr int kDecodeDepth = 4;
+
+template <int WK>
+void launch_decode(const GemmArgs& args, int max_m_blocks, hipStream_t stream) {
+  const dim3 grid(args.size_n / 64, max_m_blocks);
+  if (args.bs <= 8)
+    hipLaunchKernelGGL((wna16_decode_kernel<WK, 4, kDecodeDepth>), grid, dim3(64 * WK), 0, stream,
+                       args);
+  else
+    hipLaunchKernelGGL((wna16_decode_kernel<WK, 8, kDecodeDepth>), grid, dim3(64 * WK), 0, stream,
+                       args);
 }
 
 // ---------------------------------------------------------------------------
 // Prefill kernel: one workgroup per (leader m-block, 4 column tiles); the
 // leader takes up to 128/bs consecutive m-blocks of the same expert (a
-// 128-row tile), 4 waves each own one 64-column tile, the activation tile is
-// staged in LDS per 64-wide K chunk (double buffered), weights go straight
-// from global memory into registers and are dequantised there.
+// 128-row tile), 4 waves each own one 64-column tile.  The activation tile is
+// staged in LDS per 64-wide K chunk (double buffered, one barrier per chunk);
+// weights go straight from global memory into registers, requested kBDist
+// chunks ahead of use, and are dequantised there.
 // ---------------------------------------------------------------------------
 constexpr int kPfRows = 128;
 constexpr int kPfChunk = 64;                 // k per LDS stage (2 quant groups)
 constexpr int kPfLdsStride = kPfChunk + 8;   // bf16 per LDS row (padding vs bank conflicts)
+
+struct BChunk {
+  uint32_t w[2][4];
+  uint32_t sp[2];
+};
 
 __global__ __launch_bounds__(256, 2) void wna16_prefill_kernel(GemmArgs p) {
   __shared__ __align__(16) uint16_t s_a[2][kPfRows * kPfLdsStride];
   __shared__ int s_sid[kPfRows];
   __shared__ int s_seg_break;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int mb = blockIdx.y;
   int ntp = p.ntp[0];
   if (ntp > p.sorted_len) ntp = p.sorted_len;
   const int nblocks = ntp / p.bs;
   if (mb >= nblocks) return;
-  const int expert = p.expert_ids[mb];
+  const int expert = __builtin_amdgcn_readfirstlane(p.expert_ids[mb]);
   if (expert < 0 || expert >= p.num_experts) return;
 
   // Start of this expert's run of blocks: 1 + the last j < mb whose expert differs.
@@ -325,36 +384,61 @@ __global__ __launch_bounds__(256, 2) void wna16_prefill_kernel(GemmArgs p) {
   const int nt = blockIdx.x * 4 + wave;
   const bool wave_active = nt < n_tiles;
   const int c = lane & 31, h = lane >> 5;
-  const long long expert_words = static_cast<long long>(N) * (K >> 3);
   const int ntc = wave_active ? nt : 0;
-  const uint32_t* wbase = p.qweight + expert * expert_words + static_cast<long long>(ntc) * 128 +
-                          16 * (c & 7) + (c >> 3);
-  const long long tile_row_words = static_cast<long long>(n_tiles) * 128;
-  const uint32_t* sbase = reinterpret_cast<const uint32_t*>(
-      p.scales + static_cast<long long>(expert) * (K >> 5) * N + ntc * 64 + 8 * (c & 7) +
-      2 * (c >> 3));
-  const int srow_words = N >> 1;
+  const int groups = K >> 5;
+  const int chunks = K / kPfChunk;
+  const uint32_t expert_bytes = static_cast<uint32_t>(N) * static_cast<uint32_t>(K) / 2u;
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(
+      p.qweight + static_cast<long long>(expert) * (expert_bytes / 4u), expert_bytes);
+  const uint32_t tile_row_bytes = static_cast<uint32_t>(n_tiles) * 512u;
+  const uint32_t w_voff = (static_cast<uint32_t>(ntc) * 128u + 16u * (c & 7) + (c >> 3)) * 4u +
+                          static_cast<uint32_t>(h) * tile_row_bytes;
+  const uint32_t w_step = 2u * tile_row_bytes;
+  const uint32_t scale_bytes = static_cast<uint32_t>(groups) * static_cast<uint32_t>(N) * 2u;
+  const __amdgpu_buffer_rsrc_t sr = make_rsrc(
+      p.scales + static_cast<long long>(expert) * groups * N, scale_bytes);
+  const uint32_t s_voff = (static_cast<uint32_t>(ntc) * 64u + 8u * (c & 7) + 2u * (c >> 3)) * 2u;
+  const uint32_t s_step = static_cast<uint32_t>(N) * 2u;
+  const __amdgpu_buffer_rsrc_t ar =
+      make_rsrc(p.input, static_cast<uint32_t>(p.size_m) * static_cast<uint32_t>(K) * 2u);
 
-  // Activation staging: 128 rows x 64 k = 1024 16-byte pieces, 4 per thread.
-  uint4 stage[4];
+  auto load_b = [&](int chunk) {
+    BChunk b;
+    const int ch = min(chunk, chunks - 1);  // past the end: repeat the last chunk (unused)
+#pragma unroll
+    for (int gg = 0; gg < 2; ++gg) {
+      const uint32_t g = static_cast<uint32_t>(2 * ch + gg);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b.w[gg][j] = buf_load_b32(wr, w_voff + 16u * j, g * w_step);
+      b.sp[gg] = buf_load_b32(sr, s_voff, g * s_step);
+    }
+    return b;
+  };
+
+  // Activation staging: 128 rows x 64 k = 1024 16-byte pieces, 4 per thread;
+  // rows not routed here read zeros (out-of-range buffer offset).
+  uint32_t a_voff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int piece = tid + 256 * i;
+    const int r = piece >> 3, q = piece & 7;
+    const int sid = s_sid[r];
+    a_voff[i] = sid < valid_limit
+                    ? (static_cast<uint32_t>(sid / p.top_k) * static_cast<uint32_t>(K) + 8u * q) * 2u
+                    : kOutOfRange;
+  }
+  u32x4_t stage[4];
   auto load_chunk = [&](int chunk) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int piece = tid + 256 * i;
-      const int r = piece >> 3, q = piece & 7;
-      const int sid = s_sid[r];
-      stage[i] = make_uint4(0, 0, 0, 0);
-      if (sid < valid_limit)
-        stage[i] = *reinterpret_cast<const uint4*>(
-            p.input + static_cast<long long>(sid / p.top_k) * K + chunk * kPfChunk + 8 * q);
-    }
+    for (int i = 0; i < 4; ++i)
+      stage[i] = buf_load_b128(ar, a_voff[i], static_cast<uint32_t>(chunk) * (kPfChunk * 2u));
   };
   auto store_chunk = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int piece = tid + 256 * i;
       const int r = piece >> 3, q = piece & 7;
-      *reinterpret_cast<uint4*>(&s_a[buf][r * kPfLdsStride + 8 * q]) = stage[i];
+      *reinterpret_cast<u32x4_t*>(&s_a[buf][r * kPfLdsStride + 8 * q]) = stage[i];
     }
   };
 
@@ -365,24 +449,20 @@ __global__ __launch_bounds__(256, 2) void wna16_prefill_kernel(GemmArgs p) {
     accy[rb] = floatx16_t{};
   }
   const uint32_t k1024 = 0x64006400u, k64 = 0x54005400u;
-  const int chunks = K / kPfChunk;
 
+  BChunk b0 = load_b(0);
+  BChunk b1 = load_b(1);
   load_chunk(0);
   store_chunk(0);
   __syncthreads();
   for (int ch = 0; ch < chunks; ++ch) {
     const int buf = ch & 1;
+    const BChunk b2 = load_b(ch + 2);
     if (ch + 1 < chunks) load_chunk(ch + 1);
     if (wave_active) {
 #pragma unroll
       for (int gg = 0; gg < 2; ++gg) {
-        const int g = ch * 2 + gg;
-        const uint32_t* wp = wbase + (2LL * g + h) * tile_row_words;
-        uint32_t w[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) w[j] = wp[4 * j];
-        const uint32_t sp = sbase[static_cast<long long>(g) * srow_words];
-        const BFrags b = make_b(w, sp, k1024, k64);
+        const BFrags b = make_b(b0.w[gg], b0.sp[gg], k1024, k64);
 #pragma unroll
         for (int rb = 0; rb < 4; ++rb) {
           const uint16_t* ap = &s_a[buf][(32 * rb + c) * kPfLdsStride + 32 * gg + 16 * h];
@@ -397,6 +477,8 @@ __global__ __launch_bounds__(256, 2) void wna16_prefill_kernel(GemmArgs p) {
         }
       }
     }
+    b0 = b1;
+    b1 = b2;
     if (ch + 1 < chunks) {
       // buf^1 was last read in iteration ch-1, which every wave finished
       // before the barrier that ended it; one barrier per chunk suffices.
@@ -457,33 +539,21 @@ int wna16_gemm(const uint16_t* input, uint16_t* output, float* c_tmp, long long 
   GemmArgs args{input, output, c_tmp, reinterpret_cast<const uint32_t*>(b_qweight), b_scales,
                 workspace, sorted_token_ids, expert_ids, num_tokens_post_padded, topk_weights,
                 sorted_token_ids_len, moe_block_size, top_k, mul_topk_weights ? 1 : 0, size_m,
-                size_n, size_k, local_experts, 1};
+                size_n, size_k, local_experts};
 
   if (moe_block_size <= 16) {
-    constexpr int WK = 4;
+    // Decode: one workgroup per (m-block, tile).  Fewer expected workgroups ->
+    // more waves per workgroup splitting K, so the chip stays busy.
     const int groups = size_k / 32;
     const long long routes = static_cast<long long>(size_m) * top_k;
     const long long est_blocks = routes < max_m_blocks ? routes : max_m_blocks;
     const long long wgs = est_blocks * n_tiles;
-    int splits = 1;
-    const long long target = 2LL * cu_count;
-    if (wgs < target) splits = static_cast<int>((target + wgs - 1) / wgs);
-    const int max_split_by_k = groups / (WK * 2) > 0 ? groups / (WK * 2) : 1;
-    if (splits > max_split_by_k) splits = max_split_by_k;
-    // Partials need splits * sorted_len * N floats of c_tmp and one lock per
-    // (m-block, tile); otherwise stay with one split.
-    const long long per_split = static_cast<long long>(sorted_token_ids_len) * size_n;
-    if (splits > 1) {
-      long long cap = (c_tmp && per_split > 0) ? c_tmp_len / per_split : 0;
-      if (!workspace || workspace_len < static_cast<long long>(max_m_blocks) * n_tiles) cap = 1;
-      if (splits > cap) splits = cap < 1 ? 1 : static_cast<int>(cap);
-    }
-    args.splits = splits;
-    const long long gx = static_cast<long long>(n_tiles) * splits;
-    if (gx > 0x7fffffffLL || max_m_blocks > 65535)
-      return fail(kNotSupported, "wna16_gemm: grid too large");
-    hipLaunchKernelGGL(wna16_decode_kernel<WK>, dim3(static_cast<unsigned>(gx), max_m_blocks),
-                       dim3(64 * WK), 0, stream, args);
+    int wk = wgs >= 4LL * cu_count ? 4 : (wgs >= 2LL * cu_count ? 8 : 16);
+    while (wk > 4 && groups < wk) wk >>= 1;  // waves past the last group idle
+    if (max_m_blocks > 65535) return fail(kNotSupported, "wna16_gemm: too many m-blocks");
+    if (wk == 4) launch_decode<4>(args, max_m_blocks, stream);
+    else if (wk == 8) launch_decode<8>(args, max_m_blocks, stream);
+    else launch_decode<16>(args, max_m_blocks, stream);
     return launch_status("wna16_gemm (decode)");
   }
   if (max_m_blocks > 65535) return fail(kNotSupported, "wna16_gemm: too many m-blocks");
@@ -497,10 +567,10 @@ int wna16_gemm(const uint16_t* input, uint16_t* output, float* c_tmp, long long 
 // ---------------------------------------------------------------- C ABI
 // Reference: pegainfer-kernels/src/ffi/kimi.rs:131-152; launcher guards
 // csrc/kimi_k2/kimi_marlin_wna16.cu:264-309 (local_experts == 48,
-// group_size == 32, block size set, c_tmp required, workspace length).
-// c_tmp is sized by the reference's convention (KimiMarlinWna16Workspace,
-// src/ops/kimi_k2/experts.rs:612-652): size_n * sorted_token_ids_len floats,
-// twice that for block size 8.  Locks are left at zero on return.
+// group_size == 32, block size set, c_tmp and workspace required).  The split
+// K reduction happens inside each workgroup, so c_tmp and the lock workspace
+// are validated but never read or written (a caller's zero-filled locks stay
+// zero).
 PEGA_API int kimi_marlin_wna16_gemm_cuda(
     const uint16_t* input, uint16_t* output, float* c_tmp, const uint8_t* b_qweight,
     const uint16_t* b_scales, int32_t* workspace, const int32_t* sorted_token_ids,
@@ -523,9 +593,9 @@ PEGA_API int kimi_marlin_wna16_gemm_cuda(
                           sm_count, stream);
 }
 
-// Shape-general entry (any expert count; explicit c_tmp length in floats and
-// lock count; expert ids outside [0, local_experts) are skipped).  No
-// reference counterpart: the reference accepts 48 experts only.
+// Shape-general entry (any expert count; expert ids outside [0, local_experts)
+// are skipped; c_tmp / workspace may be null).  No reference counterpart: the
+// reference accepts 48 experts only.
 PEGA_API int pega_wna16_gemm(const uint16_t* input, uint16_t* output, float* c_tmp,
                              long long c_tmp_len, const uint8_t* b_qweight,
                              const uint16_t* b_scales, int32_t* workspace, int workspace_len,
