@@ -48,7 +48,7 @@ int kimi_moe_marlin_align_block_size_cuda(const int32_t* topk_idx, int32_t* sort
                                           int max_padded_tokens, int max_m_blocks,
                                           hipStream_t stream);
 
-/* No reference counterpart: shape-general form of the call above (local_experts <= 224,
+/* No reference counterpart: shape-general form of the call above (local_experts <= 512,
  * any topk). */
 int pega_moe_align_block_size(const int32_t* topk_idx, int32_t* sorted_token_ids,
                               int32_t* expert_ids, int32_t* num_tokens_post_padded,
@@ -144,6 +144,17 @@ int kimi_marlin_sum_topk_rows_f32_cuda(const uint16_t* route_output, float* out,
  * order), restating pegainfer-kernels/csrc/deepseek_v2_lite/dsv2_lite_moe.cu:131-155. */
 int pega_weighted_topk_sum_f32(const uint16_t* route_output, const float* topk_weight,
                                float* out, int active_tokens, int topk, int hidden_dim,
+                               hipStream_t stream);
+
+/* No reference counterpart: the top-k combine over the routes this GPU owns only
+ * (topk_idx - global_start in [0, local_experts)); the other rows of route_output are not
+ * read, so the caller skips their zero-fill (moe_nccl.rs:186-188).  topk_weight NULL: plain
+ * sum as kimi_marlin_sum_topk_rows_f32_cuda; non-NULL: fmaf chain as
+ * pega_weighted_topk_sum_f32.  Equal bit for bit to zero-filling the skipped rows and calling
+ * those (for finite weights).  hidden_dim % 8 == 0, 16-byte aligned buffers. */
+int pega_moe_combine_local_f32(const uint16_t* route_output, const int32_t* topk_idx,
+                               const float* topk_weight, float* out, int active_tokens, int topk,
+                               int hidden_dim, int global_start, int local_experts,
                                hipStream_t stream);
 
 /* Replaces kimi_residual_add_scaled_f32_cuda, pegainfer-kernels/src/ffi/kimi.rs:309-317. */

@@ -9,6 +9,7 @@
 //   kimi_residual_add_scaled_bf16_cuda    kimi_experts.cu:308-346
 //   kimi_add_f32_bf16_to_bf16_cuda        kimi_experts.cu:15-23,270-285
 //   pega_weighted_topk_sum_f32            dsv2_lite_moe.cu:131-155 (fmaf chain)
+//   pega_moe_combine_local_f32            either combine over local routes only
 #include "common.h"
 
 namespace pega {
@@ -128,6 +129,51 @@ __global__ void weighted_topk_sum_kernel(const uint16_t* __restrict__ route,
   }
 }
 
+// Top-k combine over the routes this GPU owns: route (t, k) is read only when
+// topk_idx[t*topk + k] - global_start lies in [0, local_experts).  Plain sum
+// (weights == nullptr: acc += f(r_k)) or fmaf chain (acc = fma(f(r_k), w, acc)),
+// k ascending from +0.  A skipped row would have added +0 (or fma(0, w, acc)
+// with finite w), which never changes a sum that starts at +0, so the result
+// equals the zero-filled full combine bit for bit.
+template <bool kWeighted>
+__global__ void combine_local_vec_kernel(const uint16_t* __restrict__ route,
+                                         const int32_t* __restrict__ topk_idx,
+                                         const float* __restrict__ weights,
+                                         float* __restrict__ out, int tokens, int topk,
+                                         int hidden, int global_start, int local_experts) {
+  const int per_row = hidden >> 3;
+  const long long total = static_cast<long long>(tokens) * per_row;
+  for (long long idx = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
+       idx += static_cast<long long>(gridDim.x) * blockDim.x) {
+    const long long t = idx / per_row;
+    const int d8 = static_cast<int>(idx - t * per_row) * 8;
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int k = 0; k < topk; ++k) {
+      const unsigned e = static_cast<unsigned>(topk_idx[t * topk + k] - global_start);
+      if (e >= static_cast<unsigned>(local_experts)) continue;
+      const uint4 v = *reinterpret_cast<const uint4*>(route + (t * topk + k) * hidden + d8);
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+      if (kWeighted) {
+        const float wk = weights[t * topk + k];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          acc[2 * i] = __builtin_fmaf(bf_lo(w[i]), wk, acc[2 * i]);
+          acc[2 * i + 1] = __builtin_fmaf(bf_hi(w[i]), wk, acc[2 * i + 1]);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          acc[2 * i] += bf_lo(w[i]);
+          acc[2 * i + 1] += bf_hi(w[i]);
+        }
+      }
+    }
+    float4* o = reinterpret_cast<float4*>(out + t * hidden + d8);
+    o[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    o[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+  }
+}
+
 // out = bf16( routed*scale + f(bf16(f(hidden) + f(projected))) )
 template <bool kRoutedBf16>
 __global__ void residual_add_scaled_kernel(const uint16_t* __restrict__ hidden,
@@ -237,6 +283,32 @@ PEGA_API int pega_weighted_topk_sum_f32(const uint16_t* route_output, const floa
   hipLaunchKernelGGL(weighted_topk_sum_kernel, dim3(grid), dim3(kThreads), 0, stream,
                      route_output, topk_weight, out, active_tokens, topk, hidden_dim);
   return launch_status("weighted_topk_sum");
+}
+
+// Top-k combine restricted to local routes (no reference counterpart: it
+// replaces the zero-fill of the non-local rows, moe_nccl.rs:186-188, plus
+// kimi_marlin_sum_topk_rows_f32_cuda or the weighted accumulate, with one
+// kernel that does not read those rows).
+PEGA_API int pega_moe_combine_local_f32(const uint16_t* route_output, const int32_t* topk_idx,
+                                        const float* topk_weight, float* out, int active_tokens,
+                                        int topk, int hidden_dim, int global_start,
+                                        int local_experts, hipStream_t stream) {
+  if (!route_output || !topk_idx || !out || active_tokens < 0 || topk <= 0 || hidden_dim <= 0 ||
+      local_experts <= 0)
+    return fail(kInvalidValue, "combine_local: bad arguments");
+  if (hidden_dim % 8 != 0 || !aligned16(route_output) || !aligned16(out))
+    return fail(kInvalidValue, "combine_local: hidden_dim %% 8 and 16-byte alignment required");
+  if (active_tokens == 0) return kSuccess;
+  const unsigned grid = grid_cap(static_cast<long long>(active_tokens) * (hidden_dim / 8), 1 << 20);
+  if (topk_weight)
+    hipLaunchKernelGGL(combine_local_vec_kernel<true>, dim3(grid), dim3(kThreads), 0, stream,
+                       route_output, topk_idx, topk_weight, out, active_tokens, topk, hidden_dim,
+                       global_start, local_experts);
+  else
+    hipLaunchKernelGGL(combine_local_vec_kernel<false>, dim3(grid), dim3(kThreads), 0, stream,
+                       route_output, topk_idx, topk_weight, out, active_tokens, topk, hidden_dim,
+                       global_start, local_experts);
+  return launch_status("combine_local");
 }
 
 // Reference: pegainfer-kernels/src/ffi/kimi.rs:309-317.

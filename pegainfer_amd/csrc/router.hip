@@ -20,26 +20,72 @@ namespace {
 
 constexpr int kMaxPerLane = 16;  // n_experts <= 64 * 16
 
-struct Best {
-  float v;
-  int i;
+// Order-preserving map of a float to u32 (for non-NaN values; -0 is folded
+// into +0 first, so equal floats give equal keys).  Key 0 lies below every
+// real value and marks an empty or already selected slot.
+__device__ __forceinline__ uint32_t order_key(float v) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, v + 0.0f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+template <int kCtrl, int kRowMask = 0xF>
+__device__ __forceinline__ uint32_t dpp_mov(uint32_t v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(
+      static_cast<int>(v), static_cast<int>(v), kCtrl, kRowMask, 0xF, false));
+}
+
+// Wave-wide reduction over DPP lane moves (quad swaps, half-row and row
+// mirrors, then the row-15 and row-31 broadcasts); lane 63 ends up holding
+// the result, which is read into a scalar register.
+template <typename Op>
+__device__ __forceinline__ uint32_t wave_reduce_u32(uint32_t v, Op op) {
+  v = op(v, dpp_mov<0xB1>(v));        // quad_perm [1,0,3,2]
+  v = op(v, dpp_mov<0x4E>(v));        // quad_perm [2,3,0,1]
+  v = op(v, dpp_mov<0x141>(v));       // row_half_mirror
+  v = op(v, dpp_mov<0x140>(v));       // row_mirror
+  v = op(v, dpp_mov<0x142, 0xA>(v));  // row_bcast:15 into rows 1 and 3
+  v = op(v, dpp_mov<0x143, 0xC>(v));  // row_bcast:31 into rows 2 and 3
+  return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 63));
+}
+
+struct MaxU32 {
+  __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a > b ? a : b; }
+};
+struct MinU32 {
+  __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a < b ? a : b; }
 };
 
-__device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
-  return v > bv || (v == bv && i < bi);
+__device__ __forceinline__ float lane_value(float v, int lane) {
+  return __builtin_bit_cast(float,
+                            __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
 }
 
-__device__ __forceinline__ Best wave_argmax(Best b) {
+// Index of the largest key over the wave's NS x 64 slots, ties to the lower
+// index (expert id lane + 64 j); the result is wave-uniform.
+template <int NS>
+__device__ __forceinline__ int wave_argmax(const uint32_t (&key)[NS], int lane) {
+  uint32_t best = 0;
+  int bj = 0;
 #pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) {
-    float ov = __shfl_xor(b.v, d, 64);
-    int oi = __shfl_xor(b.i, d, 64);
-    if (better(ov, oi, b.v, b.i)) { b.v = ov; b.i = oi; }
-  }
-  return b;
+  for (int j = 0; j < NS; ++j)
+    if (key[j] > best) { best = key[j]; bj = j; }  // strict: the lower slot keeps a tie
+  const uint32_t top = wave_reduce_u32(best, MaxU32{});
+  const uint32_t cand = best == top ? static_cast<uint32_t>(lane + 64 * bj) : 0xffffffffu;
+  return static_cast<int>(wave_reduce_u32(cand, MinU32{}));
 }
 
-// One wave per token; lane l owns experts l, l+64, ...
+template <int NS>
+__device__ __forceinline__ float slot_value(const float (&v)[NS], int slot) {
+  float r = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NS; ++j)
+    if (j == slot) r = v[j];
+  return r;
+}
+
+// One wave per token; lane l owns experts l, l+64, ... (NS slots per lane,
+// NS * 64 >= n_experts).
+template <int NS>
 __global__ void kimi_router_select_kernel(const float* __restrict__ logits,
                                           const float* __restrict__ bias,
                                           float* __restrict__ topk_weight,
@@ -47,46 +93,34 @@ __global__ void kimi_router_select_kernel(const float* __restrict__ logits,
                                           int n_experts, int topk, float route_scale) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  if (t >= tokens) return;
-  float score[kMaxPerLane], choice[kMaxPerLane];
+  if (t >= tokens) return;  // whole waves leave
+  float score[NS];
+  uint32_t key[NS];
 #pragma unroll
-  for (int j = 0; j < kMaxPerLane; ++j) {
+  for (int j = 0; j < NS; ++j) {
     const int e = lane + 64 * j;
     if (e < n_experts) {
       const float l = logits[static_cast<long long>(t) * n_experts + e];
       score[j] = 1.0f / (1.0f + exp_exact_f32(-l));
-      choice[j] = score[j] + bias[e];
+      key[j] = order_key(score[j] + bias[e]);
     } else {
       score[j] = 0.0f;
-      choice[j] = -__builtin_inff();
+      key[j] = 0;
     }
   }
   float sum = 0.0f;
   float my_w = 0.0f;  // lane r keeps selection r
   int my_i = 0;
   for (int r = 0; r < topk; ++r) {
-    Best b{-__builtin_inff(), n_experts};
+    const int sel = wave_argmax<NS>(key, lane);
+    const int owner = sel & 63, slot = sel >> 6;
+    const float s = lane_value(slot_value<NS>(score, slot), owner);
+    if (lane == owner) {
 #pragma unroll
-    for (int j = 0; j < kMaxPerLane; ++j) {
-      const int e = lane + 64 * j;
-      if (e < n_experts && better(choice[j], e, b.v, b.i)) { b.v = choice[j]; b.i = e; }
+      for (int j = 0; j < NS; ++j)
+        if (j == slot) key[j] = 0;
     }
-    b = wave_argmax(b);
-    float s = 0.0f;
-    if (b.i < n_experts) {
-      const int owner = b.i & 63, slot = b.i >> 6;
-      float mine = 0.0f;
-#pragma unroll
-      for (int j = 0; j < kMaxPerLane; ++j)
-        if (j == slot) mine = score[j];
-      s = __shfl(mine, owner, 64);
-      if (lane == owner) {
-#pragma unroll
-        for (int j = 0; j < kMaxPerLane; ++j)
-          if (j == slot) choice[j] = -__builtin_inff();
-      }
-    }
-    if (lane == r) { my_w = s; my_i = b.i; }
+    if (lane == r) { my_w = s; my_i = sel; }
     sum += s;
   }
   const float scale = sum > 0.0f ? route_scale / sum : 0.0f;
@@ -96,70 +130,56 @@ __global__ void kimi_router_select_kernel(const float* __restrict__ logits,
   }
 }
 
+template <int NS>
 __global__ void dsv2_router_select_kernel(const float* __restrict__ logits,
                                           float* __restrict__ topk_weight,
                                           int32_t* __restrict__ topk_idx, int tokens,
                                           int n_experts, int topk) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  if (t >= tokens) return;
-  float p[kMaxPerLane];
-  float mx = -__builtin_inff();
+  if (t >= tokens) return;  // whole waves leave
+  float p[NS];
+  uint32_t mkey = 0;
 #pragma unroll
-  for (int j = 0; j < kMaxPerLane; ++j) {
+  for (int j = 0; j < NS; ++j) {
     const int e = lane + 64 * j;
-    p[j] = e < n_experts ? logits[static_cast<long long>(t) * n_experts + e] : -__builtin_inff();
-    mx = fmaxf(mx, p[j]);
+    p[j] = e < n_experts ? logits[static_cast<long long>(t) * n_experts + e] : 0.0f;
+    if (e < n_experts) mkey = max(mkey, order_key(p[j]));
   }
+  mkey = wave_reduce_u32(mkey, MaxU32{});
+  const float mx = __builtin_bit_cast(float, (mkey & 0x80000000u) ? (mkey & 0x7fffffffu) : ~mkey);
 #pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) mx = fmaxf(mx, __shfl_xor(mx, d, 64));
-#pragma unroll
-  for (int j = 0; j < kMaxPerLane; ++j)
+  for (int j = 0; j < NS; ++j)
     p[j] = (lane + 64 * j < n_experts) ? exp_exact_f32(p[j] - mx) : 0.0f;
   // Sequential fp32 sum over experts 0, 1, 2, ... (the reference's order).
   float sum = 0.0f;
-  for (int e = 0; e < n_experts; ++e) {
-    float mine = 0.0f;
 #pragma unroll
-    for (int j = 0; j < kMaxPerLane; ++j)
-      if (j == (e >> 6)) mine = p[j];
-    sum += __shfl(mine, e & 63, 64);
+  for (int j = 0; j < NS; ++j)
+    for (int l = 0; l < 64 && 64 * j + l < n_experts; ++l) sum += lane_value(p[j], l);
+  uint32_t key[NS];
+#pragma unroll
+  for (int j = 0; j < NS; ++j) {
+    p[j] = sum == 0.0f ? 0.0f : p[j] / sum;
+    key[j] = lane + 64 * j < n_experts ? order_key(p[j]) : 0;
   }
-#pragma unroll
-  for (int j = 0; j < kMaxPerLane; ++j) p[j] = sum == 0.0f ? 0.0f : p[j] / sum;
   int my_i = 0x7fffffff;  // lane r keeps selection r
   float my_w = 0.0f;
   for (int r = 0; r < topk; ++r) {
-    Best b{-__builtin_inff(), n_experts};
+    const int sel = wave_argmax<NS>(key, lane);
+    const int owner = sel & 63, slot = sel >> 6;
+    const float w = lane_value(slot_value<NS>(p, slot), owner);
+    if (lane == owner) {
 #pragma unroll
-    for (int j = 0; j < kMaxPerLane; ++j) {
-      const int e = lane + 64 * j;
-      if (e < n_experts && better(p[j], e, b.v, b.i)) { b.v = p[j]; b.i = e; }
+      for (int j = 0; j < NS; ++j)
+        if (j == slot) key[j] = 0;
     }
-    b = wave_argmax(b);
-    float w = 0.0f;
-    if (b.i < n_experts) {
-      const int owner = b.i & 63, slot = b.i >> 6;
-      float mine = 0.0f;
-#pragma unroll
-      for (int j = 0; j < kMaxPerLane; ++j)
-        if (j == slot) mine = p[j];
-      w = __shfl(mine, owner, 64);
-      if (lane == owner) {
-#pragma unroll
-        for (int j = 0; j < kMaxPerLane; ++j)
-          if (j == slot) p[j] = -__builtin_inff();
-      }
-    }
-    if (lane == r) { my_i = b.i; my_w = w; }
+    if (lane == r) { my_i = sel; my_w = w; }
   }
   // Order the selection by expert id: a lane's rank is the number of selected
   // ids below its own (selected ids are distinct).
   int rank = 0;
-  for (int r = 0; r < topk; ++r) {
-    const int other = __shfl(my_i, r, 64);
-    rank += (other < my_i) ? 1 : 0;
-  }
+  for (int r = 0; r < topk; ++r)
+    rank += __builtin_amdgcn_readlane(my_i, r) < my_i ? 1 : 0;
   if (lane < topk) {
     topk_idx[t * topk + rank] = my_i;
     topk_weight[t * topk + rank] = my_w;
@@ -167,6 +187,37 @@ __global__ void dsv2_router_select_kernel(const float* __restrict__ logits,
 }
 
 constexpr int kWavesPerBlock = 4;
+
+// Smallest compiled slot count covering n_experts (so the per-round scans do
+// not walk empty slots: 6 for 384 experts, 1 for 64).
+template <template <int> class Launch, typename... Args>
+void launch_slots(int n_experts, Args... args) {
+  const int need = ceil_div(n_experts, 64);
+  if (need <= 1) Launch<1>::run(args...);
+  else if (need <= 2) Launch<2>::run(args...);
+  else if (need <= 4) Launch<4>::run(args...);
+  else if (need <= 6) Launch<6>::run(args...);
+  else if (need <= 8) Launch<8>::run(args...);
+  else Launch<kMaxPerLane>::run(args...);
+}
+
+template <int NS>
+struct KimiLaunch {
+  static void run(dim3 grid, hipStream_t stream, const float* logits, const float* bias, float* w,
+                  int32_t* idx, int tokens, int n_experts, int topk, float scale) {
+    hipLaunchKernelGGL(kimi_router_select_kernel<NS>, grid, dim3(64 * kWavesPerBlock), 0, stream,
+                       logits, bias, w, idx, tokens, n_experts, topk, scale);
+  }
+};
+
+template <int NS>
+struct Dsv2Launch {
+  static void run(dim3 grid, hipStream_t stream, const float* logits, float* w, int32_t* idx,
+                  int tokens, int n_experts, int topk) {
+    hipLaunchKernelGGL(dsv2_router_select_kernel<NS>, grid, dim3(64 * kWavesPerBlock), 0, stream,
+                       logits, w, idx, tokens, n_experts, topk);
+  }
+};
 
 }  // namespace
 }  // namespace pega
@@ -188,9 +239,8 @@ PEGA_API int pega_kimi_router_select(const float* logits, const float* e_score_c
     return fail(kInvalidValue, "kimi_router_select: bad shape tokens=%d experts=%d topk=%d",
                 active_tokens, n_experts, topk);
   const unsigned grid = static_cast<unsigned>(ceil_div(active_tokens, kWavesPerBlock));
-  hipLaunchKernelGGL(kimi_router_select_kernel, dim3(grid), dim3(64 * kWavesPerBlock), 0, stream,
-                     logits, e_score_correction_bias, topk_weight, topk_idx, active_tokens,
-                     n_experts, topk, route_scale);
+  launch_slots<KimiLaunch>(n_experts, dim3(grid), stream, logits, e_score_correction_bias,
+                           topk_weight, topk_idx, active_tokens, n_experts, topk, route_scale);
   return launch_status("kimi_router_select");
 }
 
@@ -204,7 +254,7 @@ PEGA_API int pega_dsv2_router_select(const float* logits, float* topk_weight, in
       topk > n_experts || topk > 64)
     return fail(kInvalidValue, "dsv2_router_select: bad shape");
   const unsigned grid = static_cast<unsigned>(ceil_div(tokens, kWavesPerBlock));
-  hipLaunchKernelGGL(dsv2_router_select_kernel, dim3(grid), dim3(64 * kWavesPerBlock), 0, stream,
-                     logits, topk_weight, topk_idx, tokens, n_experts, topk);
+  launch_slots<Dsv2Launch>(n_experts, dim3(grid), stream, logits, topk_weight, topk_idx, tokens,
+                           n_experts, topk);
   return launch_status("dsv2_router_select");
 }

@@ -11,18 +11,22 @@
 // and -1 past the total.  The reference meets this order only on its
 // single-block path (< 1024 routes); its 4-launch path takes positions from an
 // atomic cursor, so the order inside an expert varies run to run.  This
-// implementation is one deterministic launch for every size: each thread owns
-// a contiguous run of routes, a per-(thread, expert) histogram in LDS is
-// prefix-scanned down the thread axis, and the scatter walks every run in
-// order again -- a stable counting sort, bit-exact with the contract.
+// implementation is one deterministic launch of one workgroup for every size:
+// each of the 16 waves owns a contiguous run of 64-route steps; inside a step
+// the lanes holding the same expert find each other with one ballot per bit
+// of the expert id, so a lane's rank among them is a popcount.  Per-(wave,
+// expert) counts in LDS are scanned down the wave axis and across experts,
+// and the scatter replays every step in order -- a stable counting sort,
+// bit-exact with the contract.
 #include "common.h"
 
 namespace pega {
 namespace {
 
-constexpr int kAlignMaxThreads = 1024;
-constexpr int kAlignMaxExperts = 224;  // 64 threads x 224 experts x 4 B fits the LDS budget
-constexpr int kAlignLdsBudget = 56 * 1024;  // bytes of u32 per-thread histograms
+constexpr int kAlignThreads = 1024;
+constexpr int kAlignWaves = kAlignThreads / 64;
+constexpr int kAlignMaxExperts = 512;  // one thread per expert; counts take 16 x 512 x 4 B of LDS
+constexpr int kAlignBatch = 4;         // 64-route steps whose loads are in flight together
 
 __device__ __forceinline__ int wave_incl_scan(int v) {
   const int lane = threadIdx.x & 63;
@@ -44,101 +48,127 @@ __device__ __forceinline__ int segment_of(const int* start, int n, int p) {
   return lo;
 }
 
-__global__ void align_block_size_kernel(const int32_t* __restrict__ topk_idx,
-                                        int32_t* __restrict__ sorted_token_ids,
-                                        int32_t* __restrict__ expert_ids,
-                                        int32_t* __restrict__ num_tokens_post_padded,
-                                        uint32_t* __restrict__ expert_offsets,
-                                        uint32_t* __restrict__ expert_cursor, int route_elems,
-                                        int global_start, int local_experts, int block_size,
-                                        int max_padded_tokens, int max_m_blocks) {
+// Lanes of the wave holding the same local expert as this lane (valid lanes
+// only; the result is meaningless on a lane with e < 0).  One ballot per bit
+// of the id: a lane stays in the set while every bit agrees.
+__device__ __forceinline__ uint64_t same_expert_lanes(int e, int nbits) {
+  uint64_t m = __ballot(e >= 0);
+  for (int b = 0; b < nbits; ++b) {
+    const bool bit = (e >> b) & 1;
+    const uint64_t ones = __ballot(bit);
+    m &= bit ? ones : ~ones;
+  }
+  return m;
+}
+
+__global__ __launch_bounds__(kAlignThreads) void align_block_size_kernel(
+    const int32_t* __restrict__ topk_idx, int32_t* __restrict__ sorted_token_ids,
+    int32_t* __restrict__ expert_ids, int32_t* __restrict__ num_tokens_post_padded,
+    uint32_t* __restrict__ expert_offsets, uint32_t* __restrict__ expert_cursor,
+    int route_elems, int global_start, int local_experts, int block_size,
+    int max_padded_tokens, int max_m_blocks) {
   extern __shared__ __align__(16) unsigned char lds[];
   const int E = local_experts;
-  const int T = blockDim.x;
-  const int t = threadIdx.x;
-  int* seg_start = reinterpret_cast<int*>(lds);         // [E + 1]
-  int* count = seg_start + (E + 1);                      // [E]
-  uint32_t* hist = reinterpret_cast<uint32_t*>(count + E);  // [T][E]
+  uint32_t* cnt = reinterpret_cast<uint32_t*>(lds);       // [waves][E]
+  int* seg_start = reinterpret_cast<int*>(cnt + kAlignWaves * E);  // [E + 1]
+  int* wave_total = seg_start + (E + 1);                    // [waves]
+  const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
 
-  const int chunk = (route_elems + T - 1) / T;
-  const int r0 = min(t * chunk, route_elems);
-  const int r1 = min(r0 + chunk, route_elems);
-  uint32_t* my = hist + static_cast<size_t>(t) * E;
-  for (int e = 0; e < E; ++e) my[e] = 0;
-  for (int r = r0; r < r1; ++r) {
-    int e = topk_idx[r] - global_start;
-    if (e >= 0 && e < E) my[e] += 1;
+  for (int i = t; i < kAlignWaves * E; i += kAlignThreads) cnt[i] = 0;
+  const int steps = ceil_div(route_elems, 64);
+  const int per_wave = ceil_div(steps, kAlignWaves);
+  const int s0 = min(wave * per_wave, steps), s1 = min(s0 + per_wave, steps);
+  const int nbits = 32 - __builtin_clz(static_cast<unsigned>(max(E - 1, 1)));
+  const uint64_t below = (1ull << lane) - 1ull;
+  uint32_t* my_cnt = cnt + wave * E;
+  __syncthreads();
+
+  auto expert_of = [&](int r) {
+    if (r >= route_elems) return -1;
+    const int e = topk_idx[r] - global_start;
+    return (e >= 0 && e < E) ? e : -1;
+  };
+
+  // 1. per-(wave, expert) route counts; the lowest lane of each peer set adds
+  //    the set's size (peer sets have distinct experts, so no two lanes write
+  //    one counter)
+  for (int s = s0; s < s1; s += kAlignBatch) {
+    int e[kAlignBatch];
+#pragma unroll
+    for (int j = 0; j < kAlignBatch; ++j) e[j] = s + j < s1 ? expert_of((s + j) * 64 + lane) : -1;
+#pragma unroll
+    for (int j = 0; j < kAlignBatch; ++j) {
+      if (s + j >= s1) break;  // wave-uniform
+      const uint64_t peers = same_expert_lanes(e[j], nbits);
+      if (e[j] >= 0 && (peers & below) == 0) my_cnt[e[j]] += static_cast<uint32_t>(__popcll(peers));
+    }
   }
   __syncthreads();
 
-  // Exclusive scan of hist[:, e] over threads; count[e] = column total.
-  const int waves = T >> 6, wave = t >> 6, lane = t & 63;
-  const int per_lane = T >> 6;  // T is a multiple of 64
-  for (int e = wave; e < E; e += waves) {
-    int run = 0;
-    for (int i = 0; i < per_lane; ++i) run += static_cast<int>(hist[static_cast<size_t>(lane * per_lane + i) * E + e]);
-    int incl = wave_incl_scan(run);
-    int base = incl - run;
-    for (int i = 0; i < per_lane; ++i) {
-      uint32_t* cell = &hist[static_cast<size_t>(lane * per_lane + i) * E + e];
-      int c = static_cast<int>(*cell);
-      *cell = static_cast<uint32_t>(base);
-      base += c;
+  // 2. thread e: exclusive scan of its column down the waves (the column
+  //    becomes each wave's starting rank), then the padded exclusive scan of
+  //    the segment sizes across experts
+  int count = 0;
+  if (t < E) {
+    uint32_t run = 0;
+    for (int w = 0; w < kAlignWaves; ++w) {
+      const uint32_t c = cnt[w * E + t];
+      cnt[w * E + t] = run;
+      run += c;
     }
-    if (lane == 63) count[e] = incl;
+    count = static_cast<int>(run);
+  }
+  const int padded = ceil_div(count, block_size) * block_size;
+  const int incl = wave_incl_scan(padded);
+  if (lane == 63) wave_total[wave] = incl;
+  __syncthreads();
+  int before = 0, total = 0;
+  for (int w = 0; w < kAlignWaves; ++w) {
+    const int v = wave_total[w];
+    before += w < wave ? v : 0;
+    total += v;
+  }
+  if (t < E) {
+    const int start = before + incl - padded;
+    seg_start[t] = start;
+    expert_offsets[t] = static_cast<uint32_t>(start);
+    expert_cursor[t] = static_cast<uint32_t>(count);
+    // sentinels on this segment's padding
+    for (int q = start + count; q < start + padded && q < max_padded_tokens; ++q)
+      sorted_token_ids[q] = route_elems;
+  }
+  if (t == 0) {
+    seg_start[E] = total;
+    expert_offsets[E] = static_cast<uint32_t>(total);
+    num_tokens_post_padded[0] = total;
   }
   __syncthreads();
 
-  // Padded exclusive scan over experts (wave 0).
-  if (wave == 0) {
-    const int per = (E + 63) / 64;
-    int run = 0;
-    for (int i = 0; i < per; ++i) {
-      int e = lane * per + i;
-      if (e < E) run += ceil_div(count[e], block_size) * block_size;
-    }
-    int incl = wave_incl_scan(run);
-    int base = incl - run;
-    for (int i = 0; i < per; ++i) {
-      int e = lane * per + i;
-      if (e < E) {
-        seg_start[e] = base;
-        expert_offsets[e] = static_cast<uint32_t>(base);
-        expert_cursor[e] = static_cast<uint32_t>(count[e]);
-        base += ceil_div(count[e], block_size) * block_size;
+  // 3. stable scatter: replay the steps in order; a lane's slot is its
+  //    segment start + the wave's running rank + its rank among its peers,
+  //    and the lowest peer then advances the running rank
+  for (int s = s0; s < s1; s += kAlignBatch) {
+    int e[kAlignBatch];
+#pragma unroll
+    for (int j = 0; j < kAlignBatch; ++j) e[j] = s + j < s1 ? expert_of((s + j) * 64 + lane) : -1;
+#pragma unroll
+    for (int j = 0; j < kAlignBatch; ++j) {
+      if (s + j >= s1) break;  // wave-uniform
+      const uint64_t peers = same_expert_lanes(e[j], nbits);
+      if (e[j] >= 0) {
+        const uint32_t base = my_cnt[e[j]];
+        const int pos = seg_start[e[j]] + static_cast<int>(base) + __popcll(peers & below);
+        if (pos < max_padded_tokens) sorted_token_ids[pos] = (s + j) * 64 + lane;
+        if ((peers & below) == 0) my_cnt[e[j]] = base + static_cast<uint32_t>(__popcll(peers));
       }
     }
-    if (lane == 63) {
-      seg_start[E] = incl;
-      expert_offsets[E] = static_cast<uint32_t>(incl);
-      num_tokens_post_padded[0] = incl;
-    }
   }
-  __syncthreads();
 
-  // Stable scatter: this thread's routes in order, after all earlier threads'.
-  // The histogram row now holds the exclusive per-expert prefix.
-  for (int r = r0; r < r1; ++r) {
-    int e = topk_idx[r] - global_start;
-    if (e >= 0 && e < E) {
-      int pos = seg_start[e] + my[e];
-      my[e] += 1;
-      if (pos < max_padded_tokens) sorted_token_ids[pos] = r;
-    }
-  }
-  // Sentinels on padding slots and past the total; expert id per block.
-  const int total = seg_start[E];
-  for (int p = t; p < max_padded_tokens; p += T) {
-    if (p >= total) {
-      sorted_token_ids[p] = route_elems;
-    } else {
-      int e = segment_of(seg_start, E, p);
-      if (p - seg_start[e] >= count[e]) sorted_token_ids[p] = route_elems;
-    }
-  }
-  for (int b = t; b < max_m_blocks; b += T) {
-    int slot = b * block_size;
-    expert_ids[b] = slot < total ? segment_of(seg_start, E, slot) : -1;
+  // 4. sentinels past the total; expert id per block
+  for (int q = total + t; q < max_padded_tokens; q += kAlignThreads) sorted_token_ids[q] = route_elems;
+  for (int blk = t; blk < max_m_blocks; blk += kAlignThreads) {
+    const int slot = blk * block_size;
+    expert_ids[blk] = slot < total ? segment_of(seg_start, E, slot) : -1;
   }
 }
 
@@ -183,7 +213,7 @@ bool valid_block_size(int bs) { return bs == 8 || (bs >= 16 && bs <= 64 && bs % 
 
 }  // namespace
 
-// Shape-general permutation (local_experts <= 224, any topk); the Kimi
+// Shape-general permutation (local_experts <= 512, any topk); the Kimi
 // entry point below adds the reference's fixed-shape guards.
 int align_block_size(const int32_t* topk_idx, int32_t* sorted_token_ids, int32_t* expert_ids,
                      int32_t* num_tokens_post_padded, uint32_t* expert_offsets,
@@ -210,12 +240,9 @@ int align_block_size(const int32_t* topk_idx, int32_t* sorted_token_ids, int32_t
     return fail(kInvalidValue,
                 "align_block_size: capacity too small (padded %d < %lld or blocks %d < %d)",
                 max_padded_tokens, req_padded, max_m_blocks, required_blocks);
-  int threads = kAlignMaxThreads;
-  while (threads > 64 && static_cast<size_t>(threads) * local_experts * 4 > kAlignLdsBudget)
-    threads >>= 1;
-  const size_t lds = sizeof(int) * (2 * local_experts + 1) +
-                     sizeof(uint32_t) * static_cast<size_t>(threads) * local_experts;
-  hipLaunchKernelGGL(align_block_size_kernel, dim3(1), dim3(threads), lds, stream, topk_idx,
+  const size_t lds = sizeof(uint32_t) * kAlignWaves * local_experts +
+                     sizeof(int) * (local_experts + 1 + kAlignWaves);
+  hipLaunchKernelGGL(align_block_size_kernel, dim3(1), dim3(kAlignThreads), lds, stream, topk_idx,
                      sorted_token_ids, expert_ids, num_tokens_post_padded, expert_offsets,
                      expert_cursor, route_elems, global_start, local_experts, block_size,
                      max_padded_tokens, max_m_blocks);
@@ -259,7 +286,7 @@ PEGA_API int kimi_moe_marlin_align_block_size_cuda(
 }
 
 // Shape-general variant (no reference counterpart: the reference hard-codes
-// 48 experts and top-8); local_experts <= 224.  Used for the DeepSeek-V2-Lite
+// 48 experts and top-8); local_experts <= 512.  Used for the DeepSeek-V2-Lite
 // shape and one-expert cases.
 PEGA_API int pega_moe_align_block_size(const int32_t* topk_idx, int32_t* sorted_token_ids,
                                        int32_t* expert_ids, int32_t* num_tokens_post_padded,

@@ -68,9 +68,19 @@ class RoutedExperts:
         self.routing = None
 
     def forward(self, hidden: torch.Tensor, topk_idx: torch.Tensor, topk_w: torch.Tensor,
-                out_f32: torch.Tensor, combine: str = "sum", w13_timer=None) -> torch.Tensor:
-        """`w13_timer` (optional) exposes start()/stop(mark) and is called around
-        the W13 GEMM launch so a caller can time that kernel with stream events."""
+                out_f32: torch.Tensor, combine: str = "sum", w13_timer=None,
+                reference_flow: bool = False) -> torch.Tensor:
+        """Routed-expert forward (moe_nccl.rs:152-203 order: align, W13, SwiGLU, W2
+        with the top-k weight, top-k combine).
+
+        combine "sum": the weight is applied in the W2 epilogue and rows are summed
+        (Kimi); "weighted": W2 without weight and an fmaf-chain combine (DSV2).
+        reference_flow=True issues the reference's exact call sequence, zero-fills
+        included; the default skips both zero-fills (rows of routes owned by other
+        GPUs are never read: W2 reads only local rows, and the combine skips
+        non-local routes), which gives the same bits.
+        `w13_timer` (optional) exposes start()/stop(mark) and is called around the
+        W13 GEMM launch so a caller can time that kernel with stream events."""
         T = hidden.shape[0]
         rows = T * self.topk
         routing = ops.moe_align_block_size(self.route_ws, topk_idx, T, T, self.global_start)
@@ -78,21 +88,27 @@ class RoutedExperts:
         w13_out = self.w13_out[:rows]
         act = self.act[:rows]
         route_out = self.route_out[:rows]
-        w13_out.zero_()
+        if reference_flow:
+            w13_out.zero_()
         mark = w13_timer.start() if w13_timer is not None else None
         ops.wna16_gemm(self.gemm_ws, routing, hidden, self.w13, topk_w, w13_out, top_k=self.topk,
                        mul_topk_weights=False, size_m=T)
         if w13_timer is not None:
             w13_timer.stop(mark)
         ops.kimi_marlin_w13_swiglu(w13_out, act, rows, self.I)
-        route_out.zero_()
         weighted_in_gemm = combine == "sum"
+        if reference_flow:
+            route_out.zero_()
         ops.wna16_gemm(self.gemm_ws, routing, act, self.w2, topk_w, route_out, top_k=1,
                        mul_topk_weights=weighted_in_gemm, size_m=rows)
-        if weighted_in_gemm:
-            ops.kimi_marlin_sum_topk_rows_f32(route_out, T, out_f32, self.topk, self.H)
+        if reference_flow:
+            if weighted_in_gemm:
+                ops.kimi_marlin_sum_topk_rows_f32(route_out, T, out_f32, self.topk, self.H)
+            else:
+                ops.weighted_topk_sum_f32(route_out, topk_w, T, out_f32, self.topk, self.H)
         else:
-            ops.weighted_topk_sum_f32(route_out, topk_w, T, out_f32, self.topk, self.H)
+            ops.moe_combine_local_f32(route_out, topk_idx, None if weighted_in_gemm else topk_w,
+                                      T, out_f32, self.topk, self.H, self.global_start, self.E)
         return out_f32
 
 

@@ -466,6 +466,20 @@ def weighted_topk_sum_f32(route_output: torch.Tensor, topk_weight: torch.Tensor,
               active_tokens, topk, hidden, _stream())
 
 
+def moe_combine_local_f32(route_output: torch.Tensor, topk_idx: torch.Tensor,
+                          topk_weight, active_tokens: int, out: torch.Tensor, topk: int,
+                          hidden: int, global_start: int, local_experts: int) -> None:
+    """Top-k combine over local routes only (rows of other routes are not read).
+    `topk_weight` None: plain sum; a tensor: fmaf chain with those weights."""
+    _ensure(route_output.numel() >= active_tokens * topk * hidden, "route_output too small")
+    _ensure(out.numel() >= active_tokens * hidden, "combine output too small")
+    _ensure(topk_idx.dtype == torch.int32 and topk_idx.numel() >= active_tokens * topk,
+            "topk_idx must be int32 [tokens, topk]")
+    _lib.call("pega_moe_combine_local_f32", _ptr(route_output), _ptr(topk_idx),
+              None if topk_weight is None else _ptr(topk_weight), _ptr(out), active_tokens,
+              topk, hidden, global_start, local_experts, _stream())
+
+
 def kimi_residual_add_scaled_f32(hidden, projected, routed_f32, scale, out) -> None:
     n = hidden.numel()
     _ensure(projected.numel() == n and out.numel() == n, "residual_add_scaled_f32 size mismatch")

@@ -66,6 +66,32 @@ def test_weighted_topk_sum_bit_exact(oracle):
     assert np.array_equal(host(out), oracle.weighted_topk_sum(r, w, T, topk, H))
 
 
+@pytest.mark.parametrize("T,topk,H,gs,E,weighted", [(64, 8, 7168, 0, 48, False),
+                                                     (5, 8, 7168, 96, 48, False),
+                                                     (512, 6, 2048, 0, 64, True),
+                                                     (33, 6, 2048, 16, 20, True)])
+def test_combine_local_equals_zero_filled_combine(oracle, T, topk, H, gs, E, weighted):
+    """pega_moe_combine_local_f32 never reads rows of non-local routes (they hold
+    NaN here) and equals the zero-filled full combine bit for bit."""
+    from pegainfer_amd import ops
+    g = np.random.default_rng(T + topk + gs)
+    idx = g.integers(0, 384 if E == 48 else 64, size=(T, topk)).astype(np.int32)
+    local = ((idx - gs) >= 0) & ((idx - gs) < E)
+    r = _bf16_rand(g, (T * topk, H), 50.0)
+    r_garbage = r.copy()
+    r_garbage[~local.reshape(-1)] = 0x7FC0  # bf16 NaN: any read would show
+    r_zero = r.copy()
+    r_zero[~local.reshape(-1)] = 0
+    w = g.random((T, topk)).astype(np.float32)
+    out = torch.full((T, H), 7.0, dtype=torch.float32, device="cuda")
+    ops.moe_combine_local_f32(dev(r_garbage), dev(idx), dev(w) if weighted else None, T, out,
+                              topk, H, gs, E)
+    ref = (oracle.weighted_topk_sum(r_zero, w, T, topk, H) if weighted
+           else oracle.sum_topk_rows(r_zero, T, topk, H))
+    got = host(out)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
 def test_residual_joins_bit_exact(oracle):
     from pegainfer_amd import ops
     g = np.random.default_rng(3)

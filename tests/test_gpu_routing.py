@@ -79,7 +79,8 @@ def test_align_edge_cases(oracle):
 
 
 @pytest.mark.parametrize("E,topk,tokens,bs", [(64, 6, 512, 64), (1, 1, 8, 8), (1, 1, 513, 64),
-                                              (224, 8, 100, 16)])
+                                              (224, 8, 100, 16), (512, 8, 3000, 32),
+                                              (37, 3, 70000, 48)])
 def test_align_general_shapes(oracle, E, topk, tokens, bs):
     g = np.random.default_rng(E + topk)
     idx = g.integers(0, max(E, 2), size=(tokens, topk)).astype(np.int32)
@@ -134,3 +135,18 @@ def test_dsv2_router_select_bit_exact(oracle, tokens, seed):
     assert np.array_equal(host(w), ref_w)
     if tokens > 1:
         assert list(host(idx)[0]) == [7, 10, 20, 41, 54, 58]
+
+
+@pytest.mark.parametrize("n_experts,topk", [(100, 4), (200, 8), (700, 8), (1024, 16)])
+def test_kimi_router_select_expert_counts(oracle, n_experts, topk):
+    from pegainfer_amd import ops
+    g = np.random.default_rng(n_experts)
+    tokens = 33
+    logits = g.standard_normal((tokens, n_experts)).astype(np.float32)
+    bias = (g.standard_normal(n_experts) * 0.05).astype(np.float32)
+    w = torch.zeros(tokens, topk, dtype=torch.float32, device="cuda")
+    idx = torch.zeros(tokens, topk, dtype=torch.int32, device="cuda")
+    ops.kimi_router_select(dev(logits), dev(bias), w, idx, tokens, topk=topk)
+    ref_idx, ref_w = oracle.kimi_router(logits, bias, topk, 1.0)
+    assert np.array_equal(host(idx), ref_idx)
+    assert np.array_equal(host(w), ref_w)

@@ -72,6 +72,9 @@ def test_align_rejects_reference_invalid_shapes():
     # zero tokens
     rc, _ = _call("kimi_moe_marlin_align_block_size_cuda", *args, 0, 8, 96, 48, 8, 392, 49, NULL)
     assert rc == 1
+    # the shape-general entry takes up to 512 local experts (one thread each)
+    rc, msg = _call("pega_moe_align_block_size", *args, 7, 8, 0, 513, 8, 4000, 500, NULL)
+    assert rc == 1 and "E=513" in msg
 
 
 def test_gemm_rejects_reference_invalid_shapes():
