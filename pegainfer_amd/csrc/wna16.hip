@@ -332,22 +332,198 @@ void launch_decode(const GemmArgs& args, int max_m_blocks, hipStream_t stream) {
 // ---------------------------------------------------------------------------
 // Prefill kernel: one workgroup per (leader m-block, 4 column tiles); the
 // leader takes up to 128/bs consecutive m-blocks of the same expert (a
-// 128-row tile), 4 waves each own one 64-column tile.  The activation tile is
-// staged in LDS per 64-wide K chunk (double buffered, one barrier per chunk);
-// weights go straight from global memory into registers, requested kBDist
-// chunks ahead of use, and are dequantised there.
+// 128-row tile), 4 waves each own one 64-column tile.
+//
+// Per 64-wide K chunk (two quant groups):
+//   * activations: 128 rows x 64 k (16 KB) staged in double-buffered LDS
+//     (rows padded to 72 bf16 against bank conflicts), loaded by all 256
+//     threads with 16-byte buffer loads two chunks ahead of use;
+//   * weights: one 16-byte load per lane per group (the decode kernel's
+//     pattern), transposed through a per-wave LDS slot, dequantised in
+//     registers; two chunks in flight;
+//   * 16 MFMA 32x32x16 per group per wave (4 row blocks x n0/n1 x 2 k-halves).
+// The loop is unrolled by two with named ping-pong buffers, so no register
+// copies are needed to rotate the prefetch; activation loads are issued
+// before weight loads so that waiting for the former leaves the latter in
+// flight (vector-memory counters retire in order).
 // ---------------------------------------------------------------------------
 constexpr int kPfRows = 128;
 constexpr int kPfChunk = 64;                 // k per LDS stage (2 quant groups)
 constexpr int kPfLdsStride = kPfChunk + 8;   // bf16 per LDS row (padding vs bank conflicts)
 
-struct BChunk {
-  uint32_t w[2][4];
-  uint32_t sp[2];
+struct PfB {
+  u32x4_t w[2];   // per group: the 4 words (th, w = 0..3) of this lane's k-tile
+  uint32_t s[2];  // per group: this lane's two column scales
 };
 
+typedef uint16_t PfStage[kPfRows * kPfLdsStride];
+
+// Main loop and epilogue of one wave for a tile with RB routed 32-row blocks
+// (RB = 0: a wave past the last column tile, which only helps stage the
+// activations).  A compile-time RB keeps every loop body branch-free and
+// allocates only the accumulators in use.
+template <int RB>
+__device__ __forceinline__ void prefill_tile(const GemmArgs& p, PfStage* s_a, uint32_t* s_w_wave,
+                                             const int* s_sid, int expert, int nt) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int c = lane & 31, h = lane >> 5;
+  const int K = p.size_k, N = p.size_n;
+  const int n_tiles = N >> 6;
+  const int groups = K >> 5;
+  const int chunks = K / kPfChunk;
+  const int valid_limit = p.size_m * p.top_k;
+  const int ntc = RB > 0 ? nt : 0;
+  const uint32_t expert_bytes = static_cast<uint32_t>(N) * static_cast<uint32_t>(K) / 2u;
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(
+      p.qweight + static_cast<long long>(expert) * (expert_bytes / 4u), expert_bytes);
+  const uint32_t tile_row_bytes = static_cast<uint32_t>(n_tiles) * 512u;
+  const uint32_t w_voff = static_cast<uint32_t>(h) * tile_row_bytes +
+                          static_cast<uint32_t>(ntc) * 512u + static_cast<uint32_t>(c) * 16u;
+  const uint32_t w_step = 2u * tile_row_bytes;  // bytes per quant group
+  const uint32_t scale_bytes = static_cast<uint32_t>(groups) * static_cast<uint32_t>(N) * 2u;
+  const __amdgpu_buffer_rsrc_t sr = make_rsrc(
+      p.scales + static_cast<long long>(expert) * groups * N, scale_bytes);
+  const uint32_t s_voff = (static_cast<uint32_t>(ntc) * 64u + 8u * (c & 7) + 2u * (c >> 3)) * 2u;
+  const uint32_t s_step = static_cast<uint32_t>(N) * 2u;
+  const __amdgpu_buffer_rsrc_t ar =
+      make_rsrc(p.input, static_cast<uint32_t>(p.size_m) * static_cast<uint32_t>(K) * 2u);
+
+  uint32_t* slot_w = s_w_wave + h * 160 + c;          // this lane's transpose write column
+  const uint32_t* slot_r = s_w_wave + h * 160 + 4 * c;  // this lane's 16-byte read
+
+  auto load_b = [&](PfB& b, int chunk) {
+    if constexpr (RB > 0) {
+      const uint32_t ch = static_cast<uint32_t>(min(chunk, chunks - 1));  // past the end: unused
+#pragma unroll
+      for (int gg = 0; gg < 2; ++gg) {
+        const uint32_t g = 2u * ch + static_cast<uint32_t>(gg);
+        b.w[gg] = buf_load_b128(wr, w_voff, g * w_step);
+        b.s[gg] = buf_load_b32(sr, s_voff, g * s_step);
+      }
+    }
+  };
+
+  // Activation staging: 128 rows x 64 k = 1024 16-byte pieces, 4 per thread;
+  // rows not routed here read zeros (out-of-range buffer offset).
+  uint32_t a_voff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int piece = tid + 256 * i;
+    const int r = piece >> 3, q = piece & 7;
+    const int sid = s_sid[r];
+    a_voff[i] = sid < valid_limit
+                    ? (static_cast<uint32_t>(sid / p.top_k) * static_cast<uint32_t>(K) + 8u * q) * 2u
+                    : kOutOfRange;
+  }
+  // A chunk index past the end reads zeros (every lane out of range).
+  auto load_a = [&](u32x4_t (&st)[4], int chunk) {
+    const uint32_t past = chunk < chunks ? 0u : kOutOfRange;
+    const uint32_t ch = static_cast<uint32_t>(min(chunk, chunks - 1));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) st[i] = buf_load_b128(ar, a_voff[i] | past, ch * (kPfChunk * 2u));
+  };
+  // Within each 16-k block the LDS row holds k in the order
+  // {0-3, 8-11, 4-7, 12-15}: the MFMA fragments A1 (k 0-3, 8-11) and A2
+  // (k 4-7, 12-15) are then each one 16-byte LDS read, with no register moves.
+  auto store_a = [&](const u32x4_t (&st)[4], int buf) {
+    typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u32x2_t;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int piece = tid + 256 * i;
+      const int r = piece >> 3, q = piece & 7;
+      uint16_t* dst = &s_a[buf][r * kPfLdsStride + 16 * (q >> 1) + 4 * (q & 1)];
+      *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{st[i][0], st[i][1]};
+      *reinterpret_cast<u32x2_t*>(dst + 8) = u32x2_t{st[i][2], st[i][3]};
+    }
+  };
+
+  constexpr int NACC = RB > 0 ? RB : 1;
+  floatx16_t accx[NACC], accy[NACC];
+#pragma unroll
+  for (int rb = 0; rb < NACC; ++rb) {
+    accx[rb] = floatx16_t{};
+    accy[rb] = floatx16_t{};
+  }
+  const uint32_t k1024 = 0x64006400u, k64 = 0x54005400u;
+
+  auto compute = [&](const PfB& b, int buf) {
+    if constexpr (RB > 0) {
+#pragma unroll
+      for (int gg = 0; gg < 2; ++gg) {
+        // transpose the tile words into fragment order through this wave's slot
+        slot_w[0] = b.w[gg][0];
+        slot_w[32] = b.w[gg][1];
+        slot_w[64] = b.w[gg][2];
+        slot_w[96] = b.w[gg][3];
+        const u32x4_t fw = *reinterpret_cast<const u32x4_t*>(slot_r);
+        const uint32_t w4[4] = {fw[0], fw[1], fw[2], fw[3]};
+        const BFrags f = make_b(w4, b.s[gg], k1024, k64);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+          const uint16_t* ap = &s_a[buf][(32 * rb + c) * kPfLdsStride + 32 * gg + 16 * h];
+          const bf16x8_t A1 = *reinterpret_cast<const bf16x8_t*>(ap);
+          const bf16x8_t A2 = *reinterpret_cast<const bf16x8_t*>(ap + 8);
+          accx[rb] = mfma(A1, f.x1, accx[rb]);
+          accx[rb] = mfma(A2, f.x2, accx[rb]);
+          accy[rb] = mfma(A1, f.y1, accy[rb]);
+          accy[rb] = mfma(A2, f.y2, accy[rb]);
+        }
+      }
+    }
+  };
+
+  PfB b_even, b_odd;
+  u32x4_t st_even[4], st_odd[4];
+  load_a(st_even, 0);
+  load_b(b_even, 0);
+  load_a(st_odd, 1);
+  load_b(b_odd, 1);
+  store_a(st_even, 0);
+  __syncthreads();
+  // Invariant at the top of each pair: s_a[0] holds chunk ch, st_odd holds
+  // (or is loading) chunk ch + 1, b_even / b_odd hold chunks ch / ch + 1.
+  // One exit only and no tail copy of the loop body, so the accumulators
+  // keep their registers.  With an odd chunk count the last pair's second
+  // chunk is past the end: its activations are zeros, and adding +0 to an
+  // accumulator that started at +0 changes nothing.
+  const int pairs = (chunks + 1) >> 1;
+  for (int pr = 0; pr < pairs; ++pr) {
+    const int ch = 2 * pr;
+    load_a(st_even, ch + 2);
+    compute(b_even, 0);
+    load_b(b_even, ch + 2);
+    // s_a[1] was last read in the previous pair, before the barrier that ended it
+    store_a(st_odd, 1);
+    __syncthreads();
+    load_a(st_odd, ch + 3);
+    compute(b_odd, 1);
+    load_b(b_odd, ch + 3);
+    // every wave finished reading s_a[0] (chunk ch) before the barrier above;
+    // past the last chunk this stages a clamped copy nobody reads
+    store_a(st_even, 0);
+    __syncthreads();
+  }
+
+  if constexpr (RB > 0) {
+    const int n0 = nt * 64 + (c >> 3) * 16 + (c & 7);
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int row = 32 * rb + acc_row(i, h);
+        const int sid = s_sid[row];
+        if (sid < valid_limit) {
+          p.output[static_cast<long long>(sid) * N + n0] = epilogue_value(accx[rb][i], sid, p);
+          p.output[static_cast<long long>(sid) * N + n0 + 8] = epilogue_value(accy[rb][i], sid, p);
+        }
+      }
+    }
+  }
+}
+
 __global__ __launch_bounds__(256, 2) void wna16_prefill_kernel(GemmArgs p) {
-  __shared__ __align__(16) uint16_t s_a[2][kPfRows * kPfLdsStride];
+  __shared__ __align__(16) PfStage s_a[2];
+  __shared__ __align__(16) uint32_t s_w[4][kSlotDwords];
   __shared__ int s_sid[kPfRows];
   __shared__ int s_seg_break;
 
@@ -379,127 +555,22 @@ __global__ __launch_bounds__(256, 2) void wna16_prefill_kernel(GemmArgs p) {
     s_sid[r] = (r < rows) ? p.sorted_ids[mb * p.bs + r] : valid_limit;
   __syncthreads();
 
-  const int K = p.size_k, N = p.size_n;
-  const int n_tiles = N >> 6;
+  // 32-row blocks past the last routed row of the tile are skipped (an
+  // expert's padding sits at the end of its segment, so for the routing
+  // kernels' output this drops exactly the padding blocks).
+  const uint64_t lo_rows = __ballot(s_sid[lane] < valid_limit);
+  const uint64_t hi_rows = __ballot(s_sid[64 + lane] < valid_limit);
+  const int row_end = hi_rows ? 128 - __builtin_clzll(hi_rows)
+                              : (lo_rows ? 64 - __builtin_clzll(lo_rows) : 0);
   const int nt = blockIdx.x * 4 + wave;
-  const bool wave_active = nt < n_tiles;
-  const int c = lane & 31, h = lane >> 5;
-  const int ntc = wave_active ? nt : 0;
-  const int groups = K >> 5;
-  const int chunks = K / kPfChunk;
-  const uint32_t expert_bytes = static_cast<uint32_t>(N) * static_cast<uint32_t>(K) / 2u;
-  const __amdgpu_buffer_rsrc_t wr = make_rsrc(
-      p.qweight + static_cast<long long>(expert) * (expert_bytes / 4u), expert_bytes);
-  const uint32_t tile_row_bytes = static_cast<uint32_t>(n_tiles) * 512u;
-  const uint32_t w_voff = (static_cast<uint32_t>(ntc) * 128u + 16u * (c & 7) + (c >> 3)) * 4u +
-                          static_cast<uint32_t>(h) * tile_row_bytes;
-  const uint32_t w_step = 2u * tile_row_bytes;
-  const uint32_t scale_bytes = static_cast<uint32_t>(groups) * static_cast<uint32_t>(N) * 2u;
-  const __amdgpu_buffer_rsrc_t sr = make_rsrc(
-      p.scales + static_cast<long long>(expert) * groups * N, scale_bytes);
-  const uint32_t s_voff = (static_cast<uint32_t>(ntc) * 64u + 8u * (c & 7) + 2u * (c >> 3)) * 2u;
-  const uint32_t s_step = static_cast<uint32_t>(N) * 2u;
-  const __amdgpu_buffer_rsrc_t ar =
-      make_rsrc(p.input, static_cast<uint32_t>(p.size_m) * static_cast<uint32_t>(K) * 2u);
-
-  auto load_b = [&](int chunk) {
-    BChunk b;
-    const int ch = min(chunk, chunks - 1);  // past the end: repeat the last chunk (unused)
-#pragma unroll
-    for (int gg = 0; gg < 2; ++gg) {
-      const uint32_t g = static_cast<uint32_t>(2 * ch + gg);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) b.w[gg][j] = buf_load_b32(wr, w_voff + 16u * j, g * w_step);
-      b.sp[gg] = buf_load_b32(sr, s_voff, g * s_step);
-    }
-    return b;
-  };
-
-  // Activation staging: 128 rows x 64 k = 1024 16-byte pieces, 4 per thread;
-  // rows not routed here read zeros (out-of-range buffer offset).
-  uint32_t a_voff[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int piece = tid + 256 * i;
-    const int r = piece >> 3, q = piece & 7;
-    const int sid = s_sid[r];
-    a_voff[i] = sid < valid_limit
-                    ? (static_cast<uint32_t>(sid / p.top_k) * static_cast<uint32_t>(K) + 8u * q) * 2u
-                    : kOutOfRange;
-  }
-  u32x4_t stage[4];
-  auto load_chunk = [&](int chunk) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      stage[i] = buf_load_b128(ar, a_voff[i], static_cast<uint32_t>(chunk) * (kPfChunk * 2u));
-  };
-  auto store_chunk = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int piece = tid + 256 * i;
-      const int r = piece >> 3, q = piece & 7;
-      *reinterpret_cast<u32x4_t*>(&s_a[buf][r * kPfLdsStride + 8 * q]) = stage[i];
-    }
-  };
-
-  floatx16_t accx[4], accy[4];
-#pragma unroll
-  for (int rb = 0; rb < 4; ++rb) {
-    accx[rb] = floatx16_t{};
-    accy[rb] = floatx16_t{};
-  }
-  const uint32_t k1024 = 0x64006400u, k64 = 0x54005400u;
-
-  BChunk b0 = load_b(0);
-  BChunk b1 = load_b(1);
-  load_chunk(0);
-  store_chunk(0);
-  __syncthreads();
-  for (int ch = 0; ch < chunks; ++ch) {
-    const int buf = ch & 1;
-    const BChunk b2 = load_b(ch + 2);
-    if (ch + 1 < chunks) load_chunk(ch + 1);
-    if (wave_active) {
-#pragma unroll
-      for (int gg = 0; gg < 2; ++gg) {
-        const BFrags b = make_b(b0.w[gg], b0.sp[gg], k1024, k64);
-#pragma unroll
-        for (int rb = 0; rb < 4; ++rb) {
-          const uint16_t* ap = &s_a[buf][(32 * rb + c) * kPfLdsStride + 32 * gg + 16 * h];
-          const uint4 a0 = *reinterpret_cast<const uint4*>(ap);
-          const uint4 a1 = *reinterpret_cast<const uint4*>(ap + 8);
-          const bf16x8_t A1 = as_bf16x8(a0.x, a0.y, a1.x, a1.y);
-          const bf16x8_t A2 = as_bf16x8(a0.z, a0.w, a1.z, a1.w);
-          accx[rb] = mfma(A1, b.x1, accx[rb]);
-          accx[rb] = mfma(A2, b.x2, accx[rb]);
-          accy[rb] = mfma(A1, b.y1, accy[rb]);
-          accy[rb] = mfma(A2, b.y2, accy[rb]);
-        }
-      }
-    }
-    b0 = b1;
-    b1 = b2;
-    if (ch + 1 < chunks) {
-      // buf^1 was last read in iteration ch-1, which every wave finished
-      // before the barrier that ended it; one barrier per chunk suffices.
-      store_chunk(buf ^ 1);
-      __syncthreads();
-    }
-  }
-
-  if (!wave_active) return;
-  const int n0 = nt * 64 + (c >> 3) * 16 + (c & 7);
-#pragma unroll
-  for (int rb = 0; rb < 4; ++rb) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int row = 32 * rb + acc_row(i, h);
-      const int sid = s_sid[row];
-      if (sid < valid_limit) {
-        p.output[static_cast<long long>(sid) * N + n0] = epilogue_value(accx[rb][i], sid, p);
-        p.output[static_cast<long long>(sid) * N + n0 + 8] = epilogue_value(accy[rb][i], sid, p);
-      }
-    }
+  const int rb = (nt < (p.size_n >> 6)) ? __builtin_amdgcn_readfirstlane((row_end + 31) >> 5) : 0;
+  uint32_t* s_w_wave = s_w[wave];
+  switch (rb) {
+    case 0: prefill_tile<0>(p, s_a, s_w_wave, s_sid, expert, nt); break;
+    case 1: prefill_tile<1>(p, s_a, s_w_wave, s_sid, expert, nt); break;
+    case 2: prefill_tile<2>(p, s_a, s_w_wave, s_sid, expert, nt); break;
+    case 3: prefill_tile<3>(p, s_a, s_w_wave, s_sid, expert, nt); break;
+    default: prefill_tile<4>(p, s_a, s_w_wave, s_sid, expert, nt); break;
   }
 }
 
