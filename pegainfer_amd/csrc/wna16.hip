@@ -99,12 +99,15 @@ __device__ __forceinline__ BFrags make_b(const uint32_t w[4], uint32_t scale_pai
   const WordPairs q1 = dequant_word(w[1], a, b, k1024, k64);
   const WordPairs q2 = dequant_word(w[2], a, b, k1024, k64);
   const WordPairs q3 = dequant_word(w[3], a, b, k1024, k64);
-  // slot order k = {0,1,2,3,8,9,10,11} (jj 0,1) and {4,...,15} (jj 2,3)
+  // Word jj holds k = 2jj + {0, 1} in its "lo" pair and 2jj + {8, 9} in its
+  // "hi" pair, so the lo pairs of words 0..3 are k 0..7 and the hi pairs
+  // k 8..15: fragment slots follow k in memory order, and the matching
+  // activation fragments are plain 16-byte runs of the row.
   BFrags f;
-  f.x1 = as_bf16x8(q0.n0_lo, q1.n0_lo, q0.n0_hi, q1.n0_hi);
-  f.x2 = as_bf16x8(q2.n0_lo, q3.n0_lo, q2.n0_hi, q3.n0_hi);
-  f.y1 = as_bf16x8(q0.n1_lo, q1.n1_lo, q0.n1_hi, q1.n1_hi);
-  f.y2 = as_bf16x8(q2.n1_lo, q3.n1_lo, q2.n1_hi, q3.n1_hi);
+  f.x1 = as_bf16x8(q0.n0_lo, q1.n0_lo, q2.n0_lo, q3.n0_lo);
+  f.x2 = as_bf16x8(q0.n0_hi, q1.n0_hi, q2.n0_hi, q3.n0_hi);
+  f.y1 = as_bf16x8(q0.n1_lo, q1.n1_lo, q2.n1_lo, q3.n1_lo);
+  f.y2 = as_bf16x8(q0.n1_hi, q1.n1_hi, q2.n1_hi, q3.n1_hi);
   return f;
 }
 
@@ -267,8 +270,8 @@ __global__ __launch_bounds__(64 * WK) void wna16_decode_kernel(GemmArgs p) {
     const u32x4_t fw = *reinterpret_cast<const u32x4_t*>(slot_r);
     const uint32_t w4[4] = {fw[0], fw[1], fw[2], fw[3]};
     const BFrags b = make_b(w4, r.sp, k1024, k64);
-    const bf16x8_t A1 = as_bf16x8(r.a0[0], r.a0[1], r.a1[0], r.a1[1]);
-    const bf16x8_t A2 = as_bf16x8(r.a0[2], r.a0[3], r.a1[2], r.a1[3]);
+    const bf16x8_t A1 = __builtin_bit_cast(bf16x8_t, r.a0);  // k 16h + 0..7
+    const bf16x8_t A2 = __builtin_bit_cast(bf16x8_t, r.a1);  // k 16h + 8..15
     accx = mfma(A1, b.x1, accx);
     accx = mfma(A2, b.x2, accx);
     accy = mfma(A1, b.y1, accy);
@@ -422,18 +425,12 @@ __device__ __forceinline__ void prefill_tile(const GemmArgs& p, PfStage* s_a, ui
 #pragma unroll
     for (int i = 0; i < 4; ++i) st[i] = buf_load_b128(ar, a_voff[i] | past, ch * (kPfChunk * 2u));
   };
-  // Within each 16-k block the LDS row holds k in the order
-  // {0-3, 8-11, 4-7, 12-15}: the MFMA fragments A1 (k 0-3, 8-11) and A2
-  // (k 4-7, 12-15) are then each one 16-byte LDS read, with no register moves.
   auto store_a = [&](const u32x4_t (&st)[4], int buf) {
-    typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u32x2_t;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int piece = tid + 256 * i;
       const int r = piece >> 3, q = piece & 7;
-      uint16_t* dst = &s_a[buf][r * kPfLdsStride + 16 * (q >> 1) + 4 * (q & 1)];
-      *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{st[i][0], st[i][1]};
-      *reinterpret_cast<u32x2_t*>(dst + 8) = u32x2_t{st[i][2], st[i][3]};
+      *reinterpret_cast<u32x4_t*>(&s_a[buf][r * kPfLdsStride + 8 * q]) = st[i];
     }
   };
 
