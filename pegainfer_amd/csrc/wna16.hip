@@ -186,11 +186,11 @@ constexpr int kSlotDwords = 320;
 struct GroupRegs {
   u32x4_t raw;  // 4 words (th, w = 0..3) of this lane's k-tile
   uint32_t sp;
-  u32x4_t a0, a1;
+  u32x4_t a;    // activations: row c % 16, k 16h + 8(c / 16) + 0..7
 };
 
 template <int WK, int NI, int D>
-__global__ __launch_bounds__(64 * WK) void wna16_decode_kernel(GemmArgs p) {
+__global__ __launch_bounds__(64 * WK, 4) void wna16_decode_kernel(GemmArgs p) {
   __shared__ int s_sid[32];
   __shared__ float s_red[WK][2 * NI][64];
   __shared__ __align__(16) uint32_t s_w[WK][kSlotDwords];
@@ -234,12 +234,20 @@ __global__ __launch_bounds__(64 * WK) void wna16_decode_kernel(GemmArgs p) {
       p.scales + static_cast<long long>(expert) * groups * N, scale_bytes);
   const uint32_t s_voff = (static_cast<uint32_t>(nt) * 64u + 8u * (c & 7) + 2u * (c >> 3)) * 2u;
   const uint32_t s_step = static_cast<uint32_t>(N) * 2u;
-  const int my_sid = s_sid[c];
+  // Row folding: a block has at most 16 rows, so MFMA rows 16..31 are free.
+  // Lane (c, h) loads ONE 16-byte run per group: row c % 16, k 16h + 8(c/16)
+  // + 0..7.  Against the k 0..7 weight fragments (x1, y1) rows 0..15 are the
+  // real products; against the k 8..15 fragments (x2, y2) rows 16..31 are
+  // (rows 0..15 shifted by 16).  Separate lo / hi accumulators keep the
+  // unrelated halves apart, and the row's sum is lo[i] + hi[i + 8]: the same
+  // lane, 8 elements further.  One activation load per group instead of two.
+  const int my_sid = s_sid[c & 15];
   const __amdgpu_buffer_rsrc_t ar =
       make_rsrc(p.input, static_cast<uint32_t>(p.size_m) * static_cast<uint32_t>(K) * 2u);
   const uint32_t a_voff =
       my_sid < valid_limit
-          ? (static_cast<uint32_t>(my_sid / p.top_k) * static_cast<uint32_t>(K) + 16u * h) * 2u
+          ? (static_cast<uint32_t>(my_sid / p.top_k) * static_cast<uint32_t>(K) + 16u * h +
+             8u * static_cast<uint32_t>(c >> 4)) * 2u
           : kOutOfRange;
 
   uint32_t* slot_w = &s_w[wave][h * 160 + c];          // this lane's write column
@@ -251,12 +259,11 @@ __global__ __launch_bounds__(64 * WK) void wna16_decode_kernel(GemmArgs p) {
     r.sp = buf_load_b32<kStream>(sr, s_voff, static_cast<uint32_t>(g) * s_step);
     // rows not routed here have an out-of-range offset and read zeros; no
     // branch, so the loads stay in flight across groups
-    r.a0 = buf_load_b128(ar, a_voff, static_cast<uint32_t>(g) * 64u);
-    r.a1 = buf_load_b128(ar, a_voff + 16u, static_cast<uint32_t>(g) * 64u);
+    r.a = buf_load_b128(ar, a_voff, static_cast<uint32_t>(g) * 64u);
   };
 
   const uint32_t k1024 = 0x64006400u, k64 = 0x54005400u;
-  floatx16_t accx = {}, accy = {};
+  floatx16_t accx_lo = {}, accx_hi = {}, accy_lo = {}, accy_hi = {};
   GroupRegs slot[D];
 #pragma unroll
   for (int q = 0; q < D; ++q) load_group(slot[q], g0 + q < g1 ? g0 + q : g1 - 1);
@@ -270,12 +277,11 @@ __global__ __launch_bounds__(64 * WK) void wna16_decode_kernel(GemmArgs p) {
     const u32x4_t fw = *reinterpret_cast<const u32x4_t*>(slot_r);
     const uint32_t w4[4] = {fw[0], fw[1], fw[2], fw[3]};
     const BFrags b = make_b(w4, r.sp, k1024, k64);
-    const bf16x8_t A1 = __builtin_bit_cast(bf16x8_t, r.a0);  // k 16h + 0..7
-    const bf16x8_t A2 = __builtin_bit_cast(bf16x8_t, r.a1);  // k 16h + 8..15
-    accx = mfma(A1, b.x1, accx);
-    accx = mfma(A2, b.x2, accx);
-    accy = mfma(A1, b.y1, accy);
-    accy = mfma(A2, b.y2, accy);
+    const bf16x8_t A = __builtin_bit_cast(bf16x8_t, r.a);
+    accx_lo = mfma(A, b.x1, accx_lo);
+    accx_hi = mfma(A, b.x2, accx_hi);
+    accy_lo = mfma(A, b.y1, accy_lo);
+    accy_hi = mfma(A, b.y2, accy_hi);
   };
 
   // Main loop over whole rounds of D groups: no branch inside, so the loads
@@ -296,11 +302,12 @@ __global__ __launch_bounds__(64 * WK) void wna16_decode_kernel(GemmArgs p) {
     if (g + q < g1) compute_group(slot[q]);
 
   // Deterministic reduction over the WK waves (fixed order 0..WK-1); only the
-  // NI accumulator elements that hold rows < bs are exchanged.
+  // NI accumulator elements that hold rows < bs are exchanged, each the sum
+  // of its k-lo part (rows 0..15) and k-hi part (folded to rows 16..31).
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
-    s_red[wave][i][lane] = accx[i];
-    s_red[wave][NI + i][lane] = accy[i];
+    s_red[wave][i][lane] = accx_lo[i] + accx_hi[i + 8];
+    s_red[wave][NI + i][lane] = accy_lo[i] + accy_hi[i + 8];
   }
   __syncthreads();
 
