@@ -245,7 +245,7 @@ __global__ __launch_bounds__(64 * WK, 4) void wna16_decode_kernel(GemmArgs p) {
   const __amdgpu_buffer_rsrc_t ar =
       make_rsrc(p.input, static_cast<uint32_t>(p.size_m) * static_cast<uint32_t>(K) * 2u);
   const uint32_t a_voff =
-      my_sid < valid_limit
+      static_cast<unsigned>(my_sid) < static_cast<unsigned>(valid_limit)
           ? (static_cast<uint32_t>(my_sid / p.top_k) * static_cast<uint32_t>(K) + 16u * h +
              8u * static_cast<uint32_t>(c >> 4)) * 2u
           : kOutOfRange;
@@ -320,7 +320,7 @@ __global__ __launch_bounds__(64 * WK, 4) void wna16_decode_kernel(GemmArgs p) {
     const int n = (j < NI) ? n0 : n0 + 8;
     if (row < p.bs) {
       const int sid = s_sid[row];
-      if (sid < valid_limit)
+      if (static_cast<unsigned>(sid) < static_cast<unsigned>(valid_limit))
         p.output[static_cast<long long>(sid) * N + n] = epilogue_value(s, sid, p);
     }
   }
@@ -421,7 +421,7 @@ __device__ __forceinline__ void prefill_tile(const GemmArgs& p, PfStage* s_a, ui
     const int piece = tid + 256 * i;
     const int r = piece >> 3, q = piece & 7;
     const int sid = s_sid[r];
-    a_voff[i] = sid < valid_limit
+    a_voff[i] = static_cast<unsigned>(sid) < static_cast<unsigned>(valid_limit)
                     ? (static_cast<uint32_t>(sid / p.top_k) * static_cast<uint32_t>(K) + 8u * q) * 2u
                     : kOutOfRange;
   }
@@ -516,7 +516,7 @@ __device__ __forceinline__ void prefill_tile(const GemmArgs& p, PfStage* s_a, ui
       for (int i = 0; i < 16; ++i) {
         const int row = 32 * rb + acc_row(i, h);
         const int sid = s_sid[row];
-        if (sid < valid_limit) {
+        if (static_cast<unsigned>(sid) < static_cast<unsigned>(valid_limit)) {
           p.output[static_cast<long long>(sid) * N + n0] = epilogue_value(accx[rb][i], sid, p);
           p.output[static_cast<long long>(sid) * N + n0 + 8] = epilogue_value(accy[rb][i], sid, p);
         }
