@@ -34,10 +34,34 @@ namespace {
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float floatx16_t;
 
+// (x & mask) | bits in plain C, never as a vector inline-asm statement: the
+// compiler's hazard tracking cannot see VGPRs written inside asm, and a VALU
+// write landing in the destination (or a source) of an MFMA still in flight
+// is exactly the hazard it must see to insert wait states.  With `mask` in an
+// SGPR this is one v_and_or_b32 (a VOP3 on gfx9 takes no literal operand, so
+// with literal masks the compiler would emit v_and + v_or instead).
 __device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t mask, uint32_t bits) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(mask), "v"(bits));
-  return r;
+  return (x & mask) | bits;
+}
+
+// The dequant constants in registers the compiler treats as opaque: the
+// masks in SGPRs (s_mov_b32 in an asm statement that writes only SGPRs, which
+// no MFMA reads) and the fp16 bias patterns in VGPRs (a DPP move of a
+// wave-uniform value, which the compiler does not fold).  v_and_or_b32 then
+// takes one SGPR and one VGPR operand, within gfx9's one-scalar-operand limit.
+struct DqConst {
+  uint32_t m_lo, m_hi;  // 0x000F000F, 0x00F000F0
+  uint32_t k1024, k64;  // fp16 1024 | 1024 and 64 | 64
+};
+__device__ __forceinline__ DqConst dq_consts() {
+  uint32_t lo, hi;
+  asm("s_mov_b32 %0, 0x000f000f" : "=s"(lo));
+  asm("s_mov_b32 %0, 0x00f000f0" : "=s"(hi));
+  const uint32_t k1024 = static_cast<uint32_t>(
+      __builtin_amdgcn_mov_dpp(static_cast<int>(0x64006400u), 0xB1, 0xF, 0xF, true));
+  const uint32_t k64 = static_cast<uint32_t>(
+      __builtin_amdgcn_mov_dpp(static_cast<int>(0x54005400u), 0xB1, 0xF, 0xF, true));
+  return DqConst{lo, hi, k1024, k64};
 }
 
 __device__ __forceinline__ float h_lo(uint32_t p) {
@@ -61,13 +85,12 @@ struct WordPairs {
 };
 
 __device__ __forceinline__ WordPairs dequant_word(uint32_t x, const ColScale& a,
-                                                  const ColScale& b, uint32_t k1024,
-                                                  uint32_t k64) {
-  const uint32_t p0 = and_or(x, 0x000F000Fu, k1024);
-  const uint32_t p1 = and_or(x, 0x00F000F0u, k64);
+                                                  const ColScale& b, const DqConst& k) {
+  const uint32_t p0 = and_or(x, k.m_lo, k.k1024);
+  const uint32_t p1 = and_or(x, k.m_hi, k.k64);
   const uint32_t y = x >> 8;
-  const uint32_t p2 = and_or(y, 0x000F000Fu, k1024);
-  const uint32_t p3 = and_or(y, 0x00F000F0u, k64);
+  const uint32_t p2 = and_or(y, k.m_lo, k.k1024);
+  const uint32_t p3 = and_or(y, k.m_hi, k.k64);
   WordPairs r;
   r.n0_lo = pack_bf16x2(__builtin_fmaf(h_lo(p0), a.s, a.c1024), __builtin_fmaf(h_hi(p0), a.s, a.c1024));
   r.n0_hi = pack_bf16x2(__builtin_fmaf(h_lo(p1), a.s, a.c72), __builtin_fmaf(h_hi(p1), a.s, a.c72));
@@ -92,13 +115,13 @@ struct BFrags {
 };
 
 __device__ __forceinline__ BFrags make_b(const uint32_t w[4], uint32_t scale_pair,
-                                         uint32_t k1024, uint32_t k64) {
+                                         const DqConst& k) {
   const ColScale a = col_scale(bf_lo(scale_pair));
   const ColScale b = col_scale(bf_hi(scale_pair));
-  const WordPairs q0 = dequant_word(w[0], a, b, k1024, k64);
-  const WordPairs q1 = dequant_word(w[1], a, b, k1024, k64);
-  const WordPairs q2 = dequant_word(w[2], a, b, k1024, k64);
-  const WordPairs q3 = dequant_word(w[3], a, b, k1024, k64);
+  const WordPairs q0 = dequant_word(w[0], a, b, k);
+  const WordPairs q1 = dequant_word(w[1], a, b, k);
+  const WordPairs q2 = dequant_word(w[2], a, b, k);
+  const WordPairs q3 = dequant_word(w[3], a, b, k);
   // Word jj holds k = 2jj + {0, 1} in its "lo" pair and 2jj + {8, 9} in its
   // "hi" pair, so the lo pairs of words 0..3 are k 0..7 and the hi pairs
   // k 8..15: fragment slots follow k in memory order, and the matching
@@ -262,7 +285,7 @@ __global__ __launch_bounds__(64 * WK, 4) void wna16_decode_kernel(GemmArgs p) {
     r.a = buf_load_b128(ar, a_voff, static_cast<uint32_t>(g) * 64u);
   };
 
-  const uint32_t k1024 = 0x64006400u, k64 = 0x54005400u;
+  const DqConst dq = dq_consts();
   floatx16_t accx_lo = {}, accx_hi = {}, accy_lo = {}, accy_hi = {};
   GroupRegs slot[D];
 #pragma unroll
@@ -276,7 +299,7 @@ __global__ __launch_bounds__(64 * WK, 4) void wna16_decode_kernel(GemmArgs p) {
     slot_w[96] = r.raw[3];
     const u32x4_t fw = *reinterpret_cast<const u32x4_t*>(slot_r);
     const uint32_t w4[4] = {fw[0], fw[1], fw[2], fw[3]};
-    const BFrags b = make_b(w4, r.sp, k1024, k64);
+    const BFrags b = make_b(w4, r.sp, dq);
     const bf16x8_t A = __builtin_bit_cast(bf16x8_t, r.a);
     accx_lo = mfma(A, b.x1, accx_lo);
     accx_hi = mfma(A, b.x2, accx_hi);
@@ -448,7 +471,7 @@ __device__ __forceinline__ void prefill_tile(const GemmArgs& p, PfStage* s_a, ui
     accx[rb] = floatx16_t{};
     accy[rb] = floatx16_t{};
   }
-  const uint32_t k1024 = 0x64006400u, k64 = 0x54005400u;
+  const DqConst dq = dq_consts();
 
   auto compute = [&](const PfB& b, int buf) {
     if constexpr (RB > 0) {
@@ -461,7 +484,7 @@ __device__ __forceinline__ void prefill_tile(const GemmArgs& p, PfStage* s_a, ui
         slot_w[96] = b.w[gg][3];
         const u32x4_t fw = *reinterpret_cast<const u32x4_t*>(slot_r);
         const uint32_t w4[4] = {fw[0], fw[1], fw[2], fw[3]};
-        const BFrags f = make_b(w4, b.s[gg], k1024, k64);
+        const BFrags f = make_b(w4, b.s[gg], dq);
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
           const uint16_t* ap = &s_a[buf][(32 * rb + c) * kPfLdsStride + 32 * gg + 16 * h];

@@ -100,9 +100,9 @@ def test_gemm_random_kimi_entry(oracle, bs, topk, mul, T):
 @pytest.mark.parametrize("rows,N,K,splits", [(1, 9728, 2560, 8), (4, 4096, 7168, 8),
                                              (8, 7168, 2048, 8), (3, 512, 1024, 1)])
 def test_gemm_dense_split_k(oracle, rows, N, K, splits):
-    """One expert (C1/C2 shapes) through the shape-general entry; cross-workgroup
-    split-K with the deterministic last-arriver reduction; called twice so the
-    second call proves the locks were reset."""
+    """One expert (C1/C2 shapes) through the shape-general entry, whose c_tmp
+    may be larger than the reference's (`splits`); called twice, and the lock
+    workspace is never written."""
     g = np.random.default_rng(rows * 7 + N)
     q = g.integers(-8, 8, size=(1, N, K))
     scale_bits = oracle.f32_to_bf16((np.abs(g.standard_normal((1, N, K // 32))) * 0.02 / 7).astype(np.float32))
@@ -126,3 +126,45 @@ def test_gemm_deterministic_across_runs(oracle):
                       scale_bits=scale_bits, idx=idx, tw=np.ones((T, 8), np.float32))
         outs.append(got)
     assert np.array_equal(outs[0], outs[1])
+
+
+@pytest.mark.parametrize("rows,N,K", [(1, 9728, 2560), (8, 4096, 7168)])
+def test_gemm_small_batch_exact_and_deterministic(oracle, rows, N, K):
+    """Decode of one expert at a small batch (16 waves split K inside each
+    workgroup) on a case whose every partial sum is exact (small-integer
+    activations, power-of-two scales): bit-exact with the oracle, and
+    identical across calls.  Also a regression test for a wrong-result bug in
+    the bs <= 8 decode variant: a dequant step written as a vector inline-asm
+    statement hid a register write from the compiler's MFMA hazard tracking,
+    and it landed in an MFMA destination still in flight."""
+    g = np.random.default_rng(rows + K)
+    q = g.integers(-8, 8, size=(1, N, K))
+    scale_bits = oracle.f32_to_bf16(
+        (2.0 ** g.integers(-6, -2, size=(1, N, K // 32))).astype(np.float32))
+    a_bits = oracle.f32_to_bf16(g.integers(-2, 3, size=(rows, K)).astype(np.float32))
+    outs = []
+    for _ in range(2):
+        got, ref = _run(oracle, E=1, N=N, K=K, T=rows, topk=1, bs=8, mul=False, a_bits=a_bits,
+                        q=q, scale_bits=scale_bits, idx=np.zeros((rows, 1)),
+                        tw=np.ones((rows, 1), np.float32), extra_splits=8)
+        assert np.array_equal(got, ref)
+        outs.append(got)
+    assert np.array_equal(outs[0], outs[1])
+
+
+def test_gemm_block8_four_waves_exact(oracle):
+    """Block size 8 with enough workgroups that 4 waves split K (the bs <= 8,
+    4-wave decode variant, main prefetch loop included: 20 groups per wave),
+    48 experts through the reference entry, exact inputs: bit-exact.  This is
+    the configuration in which the inline-asm hazard above corrupted the
+    n0 columns."""
+    g = np.random.default_rng(77)
+    E, N, K, T = 48, 2048, 2560, 8
+    q = g.integers(-8, 8, size=(E, N, K))
+    scale_bits = oracle.f32_to_bf16(
+        (2.0 ** g.integers(-6, -2, size=(E, N, K // 32))).astype(np.float32))
+    a_bits = oracle.f32_to_bf16(g.integers(-2, 3, size=(T, K)).astype(np.float32))
+    idx = g.integers(0, 48, size=(T, 8))
+    got, ref = _run(oracle, E=E, N=N, K=K, T=T, topk=8, bs=8, mul=False, a_bits=a_bits, q=q,
+                    scale_bits=scale_bits, idx=idx, tw=np.ones((T, 8), np.float32), threads=16)
+    assert np.array_equal(got, ref)
