@@ -185,3 +185,22 @@ class Dsv2MoeLayer:
         self.shared.forward(hidden, self.shared_out[:T])
         ops.kimi_add_f32_bf16_to_bf16(self.routed_f32[:T], self.shared_out[:T], out)
         return out
+
+
+def capture_graph(step, warmup: int = 2) -> torch.cuda.CUDAGraph:
+    """Capture `step()` (a sequence of this library's launches on the current
+    stream) into a HIP graph, as a decode loop replays a layer.  The step is
+    run `warmup` times on a side stream first, so every lazily cached device
+    query happens outside the capture.  The captured launches contain no
+    memset nodes: the default RoutedExperts flow writes every output element it
+    later reads and clears nothing."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(warmup):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    return graph
