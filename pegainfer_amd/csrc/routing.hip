@@ -26,7 +26,7 @@ namespace {
 constexpr int kAlignThreads = 1024;
 constexpr int kAlignWaves = kAlignThreads / 64;
 constexpr int kAlignMaxExperts = 512;  // one thread per expert; counts take 16 x 512 x 4 B of LDS
-constexpr int kAlignBatch = 4;         // 64-route steps whose loads are in flight together
+constexpr int kAlignBatch = 16;        // 64-route steps whose loads are in flight together
 
 __device__ __forceinline__ int wave_incl_scan(int v) {
   const int lane = threadIdx.x & 63;
@@ -98,9 +98,11 @@ __global__ __launch_bounds__(kAlignThreads) void align_block_size_kernel(
     for (int j = 0; j < kAlignBatch; ++j) e[j] = s + j < s1 ? expert_of((s + j) * 64 + lane) : -1;
 #pragma unroll
     for (int j = 0; j < kAlignBatch; ++j) {
-      if (s + j >= s1) break;  // wave-uniform
-      const uint64_t peers = same_expert_lanes(e[j], nbits);
-      if (e[j] >= 0 && (peers & below) == 0) my_cnt[e[j]] += static_cast<uint32_t>(__popcll(peers));
+      if (s + j < s1) {  // wave-uniform
+        const uint64_t peers = same_expert_lanes(e[j], nbits);
+        if (e[j] >= 0 && (peers & below) == 0)
+          my_cnt[e[j]] += static_cast<uint32_t>(__popcll(peers));
+      }
     }
   }
   __syncthreads();
@@ -153,7 +155,7 @@ __global__ __launch_bounds__(kAlignThreads) void align_block_size_kernel(
     for (int j = 0; j < kAlignBatch; ++j) e[j] = s + j < s1 ? expert_of((s + j) * 64 + lane) : -1;
 #pragma unroll
     for (int j = 0; j < kAlignBatch; ++j) {
-      if (s + j >= s1) break;  // wave-uniform
+      if (s + j >= s1) continue;  // wave-uniform
       const uint64_t peers = same_expert_lanes(e[j], nbits);
       if (e[j] >= 0) {
         const uint32_t base = my_cnt[e[j]];
