@@ -65,6 +65,14 @@ __device__ __forceinline__ float exp_exact_f32(float x) {
   return static_cast<float>(::exp(static_cast<double>(x)));
 }
 
+// SwiGLU of one column pair: bf16( f(bf16(g / (1 + e^-g))) * u ), g = gate,
+// u = up (pegainfer-kernels/csrc/kimi_k2/kimi_marlin_wna16.cu:345-361).
+__device__ __forceinline__ uint16_t swiglu_one(float g, float u) {
+  const float e = (g == 0.0f) ? 1.0f : exp_exact_f32(-g);
+  const float silu = g / (1.0f + e);
+  return f2bf(bf2f(f2bf(silu)) * u);
+}
+
 __host__ __device__ constexpr int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
 }  // namespace pega

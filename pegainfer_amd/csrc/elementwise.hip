@@ -15,13 +15,6 @@
 namespace pega {
 namespace {
 
-// out = bf16( f(bf16(g / (1 + e^-g))) * u ), g = gate column, u = up column.
-__device__ __forceinline__ uint16_t swiglu_one(float g, float u) {
-  const float e = (g == 0.0f) ? 1.0f : exp_exact_f32(-g);
-  const float silu = g / (1.0f + e);
-  return f2bf(bf2f(f2bf(silu)) * u);
-}
-
 __device__ __forceinline__ void swiglu8(const uint16_t* __restrict__ row, uint16_t* __restrict__ out,
                                         int inter, int c8) {
   const uint4 g = *reinterpret_cast<const uint4*>(row + c8);

@@ -150,6 +150,9 @@ struct GemmArgs {
   const float* topk_w;
   int sorted_len, bs, top_k, mul, size_m, size_n, size_k;
   int num_experts;  // expert ids outside [0, num_experts) are skipped
+  int splits;       // decode: K split across `splits` workgroups (partial != nullptr)
+  float* partial;   // non-null: fp32 partial sums [splits][size_m * top_k][size_n]
+                    // instead of the bf16 output (finished by the consumer kernel)
 };
 
 __device__ __forceinline__ uint16_t epilogue_value(float acc, int sid, const GemmArgs& p) {
@@ -218,7 +221,9 @@ __global__ __launch_bounds__(64 * WK, 4) void wna16_decode_kernel(GemmArgs p) {
   __shared__ float s_red[WK][2 * NI][64];
   __shared__ __align__(16) uint32_t s_w[WK][kSlotDwords];
 
-  const int nt = blockIdx.x;
+  const int n_tiles = p.size_n >> 6;
+  const int nt = blockIdx.x % n_tiles;
+  const int split = blockIdx.x / n_tiles;
   const int mb = blockIdx.y;
   int ntp = p.ntp[0];
   if (ntp > p.sorted_len) ntp = p.sorted_len;
@@ -241,9 +246,10 @@ __global__ __launch_bounds__(64 * WK, 4) void wna16_decode_kernel(GemmArgs p) {
 
   const int c = lane & 31, h = lane >> 5;
   const int K = p.size_k, N = p.size_n;
-  const int n_tiles = N >> 6;
   const int groups = K >> 5;
-  const int g0 = (groups * wave) / WK, g1 = (groups * (wave + 1)) / WK;
+  // this workgroup's share of the K groups, then this wave's share of that
+  const int gs0 = (groups * split) / p.splits, gs1 = (groups * (split + 1)) / p.splits;
+  const int g0 = gs0 + ((gs1 - gs0) * wave) / WK, g1 = gs0 + ((gs1 - gs0) * (wave + 1)) / WK;
 
   const uint32_t expert_bytes = static_cast<uint32_t>(N) * static_cast<uint32_t>(K) / 2u;
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(
@@ -343,8 +349,12 @@ __global__ __launch_bounds__(64 * WK, 4) void wna16_decode_kernel(GemmArgs p) {
     const int n = (j < NI) ? n0 : n0 + 8;
     if (row < p.bs) {
       const int sid = s_sid[row];
-      if (static_cast<unsigned>(sid) < static_cast<unsigned>(valid_limit))
-        p.output[static_cast<long long>(sid) * N + n] = epilogue_value(s, sid, p);
+      if (static_cast<unsigned>(sid) < static_cast<unsigned>(valid_limit)) {
+        if (p.partial)
+          p.partial[(static_cast<long long>(split) * valid_limit + sid) * N + n] = s;
+        else
+          p.output[static_cast<long long>(sid) * N + n] = epilogue_value(s, sid, p);
+      }
     }
   }
 }
@@ -353,7 +363,7 @@ constexpr int kDecodeDepth = 4;
 
 template <int WK>
 void launch_decode(const GemmArgs& args, int max_m_blocks, hipStream_t stream) {
-  const dim3 grid(args.size_n / 64, max_m_blocks);
+  const dim3 grid(args.size_n / 64 * args.splits, max_m_blocks);
   if (args.bs <= 8)
     hipLaunchKernelGGL((wna16_decode_kernel<WK, 4, kDecodeDepth>), grid, dim3(64 * WK), 0, stream,
                        args);
@@ -601,6 +611,50 @@ __global__ __launch_bounds__(256, 2) void wna16_prefill_kernel(GemmArgs p) {
   }
 }
 
+// W13 finish fused with SwiGLU: for every routed row, the gate and up
+// columns are the sums of the K shares' fp32 partials (share order, so the
+// result does not depend on scheduling), rounded to bf16 exactly as the W13
+// output would be, then SwiGLU as in kimi_marlin_w13_swiglu_cuda.  One thread
+// per 8 columns of a row.
+__global__ void w13_swiglu_partials_kernel(GemmArgs p, uint16_t* __restrict__ act, int inter) {
+  int ntp = p.ntp[0];
+  if (ntp > p.sorted_len) ntp = p.sorted_len;
+  const int per_row = inter >> 3;
+  const int N = p.size_n;
+  const int valid_limit = p.size_m * p.top_k;
+  const long long total = static_cast<long long>(ntp) * per_row;
+  for (long long idx = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
+       idx += static_cast<long long>(gridDim.x) * blockDim.x) {
+    const int pos = static_cast<int>(idx / per_row);
+    const int c8 = static_cast<int>(idx - static_cast<long long>(pos) * per_row) * 8;
+    const int sid = p.sorted_ids[pos];
+    if (static_cast<unsigned>(sid) >= static_cast<unsigned>(valid_limit)) continue;
+    const int e = p.expert_ids[pos / p.bs];
+    if (e < 0 || e >= p.num_experts) continue;
+    float g[8] = {0, 0, 0, 0, 0, 0, 0, 0}, u[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int sp = 0; sp < p.splits; ++sp) {
+      const float* row = p.partial + (static_cast<long long>(sp) * valid_limit + sid) * N;
+      const float4 g0 = *reinterpret_cast<const float4*>(row + c8);
+      const float4 g1 = *reinterpret_cast<const float4*>(row + c8 + 4);
+      const float4 u0 = *reinterpret_cast<const float4*>(row + inter + c8);
+      const float4 u1 = *reinterpret_cast<const float4*>(row + inter + c8 + 4);
+      g[0] += g0.x; g[1] += g0.y; g[2] += g0.z; g[3] += g0.w;
+      g[4] += g1.x; g[5] += g1.y; g[6] += g1.z; g[7] += g1.w;
+      u[0] += u0.x; u[1] += u0.y; u[2] += u0.z; u[3] += u0.w;
+      u[4] += u1.x; u[5] += u1.y; u[6] += u1.z; u[7] += u1.w;
+    }
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint16_t lo = swiglu_one(bf2f(f2bf(g[2 * i])), bf2f(f2bf(u[2 * i])));
+      const uint16_t hi = swiglu_one(bf2f(f2bf(g[2 * i + 1])), bf2f(f2bf(u[2 * i + 1])));
+      w[i] = static_cast<uint32_t>(lo) | (static_cast<uint32_t>(hi) << 16);
+    }
+    *reinterpret_cast<uint4*>(act + static_cast<long long>(sid) * inter + c8) =
+        make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
 bool valid_block_size(int bs) { return bs == 8 || (bs >= 16 && bs <= 64 && bs % 16 == 0); }
 
 }  // namespace
@@ -637,7 +691,7 @@ int wna16_gemm(const uint16_t* input, uint16_t* output, float* c_tmp, long long 
   GemmArgs args{input, output, c_tmp, reinterpret_cast<const uint32_t*>(b_qweight), b_scales,
                 workspace, sorted_token_ids, expert_ids, num_tokens_post_padded, topk_weights,
                 sorted_token_ids_len, moe_block_size, top_k, mul_topk_weights ? 1 : 0, size_m,
-                size_n, size_k, local_experts};
+                size_n, size_k, local_experts, 1, nullptr};
 
   if (moe_block_size <= 16) {
     // Decode: one workgroup per (m-block, tile).  Fewer expected workgroups ->
@@ -658,6 +712,71 @@ int wna16_gemm(const uint16_t* input, uint16_t* output, float* c_tmp, long long 
   hipLaunchKernelGGL(wna16_prefill_kernel, dim3(ceil_div(n_tiles, 4), max_m_blocks), dim3(256),
                      0, stream, args);
   return launch_status("wna16_gemm (prefill)");
+}
+
+// W13 GEMM + SwiGLU for the small-batch decode path (block size <= 16).  The
+// few (m-block, tile) workgroups of a small batch are multiplied by splitting
+// K across workgroups; their fp32 partials go to `partials` and the SwiGLU
+// kernel sums them, so the split costs no extra launch and no cross-workgroup
+// synchronisation.
+int wna16_w13_swiglu(const uint16_t* input, uint16_t* act, float* partials, long long partials_len,
+                     const uint8_t* b_qweight, const uint16_t* b_scales,
+                     const int32_t* sorted_token_ids, const int32_t* expert_ids,
+                     const int32_t* num_tokens_post_padded, int sorted_token_ids_len,
+                     int moe_block_size, int top_k, int size_m, int inter, int size_k,
+                     int local_experts, int group_size, int cu_count, hipStream_t stream) {
+  if (!input || !act || !partials || !b_qweight || !b_scales || !sorted_token_ids ||
+      !expert_ids || !num_tokens_post_padded)
+    return fail(kInvalidValue, "w13_swiglu: null pointer");
+  if (group_size != 32 || top_k <= 0 || size_m <= 0 || inter <= 0 || size_k <= 0 ||
+      sorted_token_ids_len <= 0 || local_experts <= 0)
+    return fail(kInvalidValue, "w13_swiglu: bad shape m=%d inter=%d k=%d", size_m, inter, size_k);
+  if (moe_block_size != 8 && moe_block_size != 16)
+    return fail(kInvalidValue, "w13_swiglu: block size %d not in {8, 16}", moe_block_size);
+  const int size_n = 2 * inter;
+  if (size_k % 64 != 0 || inter % 64 != 0)
+    return fail(kNotSupported, "w13_swiglu: size_k %% 64 and inter %% 64 must be 0");
+  if ((reinterpret_cast<uintptr_t>(input) & 15u) != 0 ||
+      (reinterpret_cast<uintptr_t>(act) & 15u) != 0 ||
+      (reinterpret_cast<uintptr_t>(partials) & 15u) != 0)
+    return fail(kInvalidValue, "w13_swiglu: input, act and partials must be 16-byte aligned");
+  const long long routes = static_cast<long long>(size_m) * top_k;
+  if (partials_len < routes * size_n)
+    return fail(kInvalidValue, "w13_swiglu: partials holds %lld floats, needs >= %lld",
+                partials_len, routes * size_n);
+  if (cu_count <= 0) cu_count = current_cu_count();
+  if (cu_count <= 0) return fail(kInvalidValue, "w13_swiglu: no device");
+
+  const int max_m_blocks = ceil_div(sorted_token_ids_len, moe_block_size);
+  if (max_m_blocks > 65535) return fail(kNotSupported, "w13_swiglu: too many m-blocks");
+  const int n_tiles = size_n / 64;
+  const int groups = size_k / 32;
+  const long long est_blocks = routes < max_m_blocks ? routes : max_m_blocks;
+  const long long wgs = est_blocks * n_tiles;
+  // shares: about two workgroups per CU, at least 8 groups (two per wave) each
+  long long sp = (2LL * cu_count + wgs - 1) / wgs;
+  if (sp > 16) sp = 16;
+  if (sp > groups / 8) sp = groups / 8;
+  if (sp > partials_len / (routes * size_n)) sp = partials_len / (routes * size_n);
+  const int splits = sp > 1 ? static_cast<int>(sp) : 1;
+  GemmArgs args{input, nullptr, nullptr, reinterpret_cast<const uint32_t*>(b_qweight), b_scales,
+                nullptr, sorted_token_ids, expert_ids, num_tokens_post_padded, nullptr,
+                sorted_token_ids_len, moe_block_size, top_k, 0, size_m, size_n, size_k,
+                local_experts, splits, partials};
+  const long long total_wgs = wgs * splits;
+  int wk = total_wgs >= 4LL * cu_count ? 4 : (total_wgs >= 2LL * cu_count ? 8 : 16);
+  while (wk > 4 && groups / splits < 2 * wk) wk >>= 1;  // keep >= 2 groups per wave
+  if (wk == 4) launch_decode<4>(args, max_m_blocks, stream);
+  else if (wk == 8) launch_decode<8>(args, max_m_blocks, stream);
+  else launch_decode<16>(args, max_m_blocks, stream);
+  const int rc = launch_status("w13_swiglu (GEMM)");
+  if (rc != kSuccess) return rc;
+  const long long work = static_cast<long long>(sorted_token_ids_len) * (inter / 8);
+  long long grid = (work + 255) / 256;
+  if (grid > 4LL * cu_count) grid = 4LL * cu_count;
+  hipLaunchKernelGGL(w13_swiglu_partials_kernel, dim3(static_cast<unsigned>(grid)), dim3(256), 0,
+                     stream, args, act, inter);
+  return launch_status("w13_swiglu (SwiGLU)");
 }
 
 }  // namespace pega
@@ -708,4 +827,21 @@ PEGA_API int pega_wna16_gemm(const uint16_t* input, uint16_t* output, float* c_t
                           topk_weights, sorted_token_ids_len, moe_block_size, top_k,
                           mul_topk_weights, size_m, size_n, size_k, local_experts, group_size,
                           sm_count, stream);
+}
+
+// Fused W13 + SwiGLU for the small-batch decode path (no reference symbol: the
+// reference runs kimi_marlin_wna16_gemm_cuda then kimi_marlin_w13_swiglu_cuda).
+PEGA_API int pega_wna16_w13_swiglu(const uint16_t* input, uint16_t* act, float* partials,
+                                   long long partials_len, const uint8_t* b_qweight,
+                                   const uint16_t* b_scales, const int32_t* sorted_token_ids,
+                                   const int32_t* expert_ids,
+                                   const int32_t* num_tokens_post_padded,
+                                   int sorted_token_ids_len, int moe_block_size, int top_k,
+                                   int size_m, int intermediate_dim, int size_k, int local_experts,
+                                   int group_size, int sm_count, hipStream_t stream) {
+  return pega::wna16_w13_swiglu(input, act, partials, partials_len, b_qweight, b_scales,
+                                sorted_token_ids, expert_ids, num_tokens_post_padded,
+                                sorted_token_ids_len, moe_block_size, top_k, size_m,
+                                intermediate_dim, size_k, local_experts, group_size, sm_count,
+                                stream);
 }

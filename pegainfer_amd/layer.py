@@ -156,10 +156,19 @@ class ExpertFFN:
         self.h13 = torch.zeros(max_rows, w13.out_dim, **bf)
         self.act = torch.zeros(max_rows, self.I, **bf)
 
-    def forward(self, x: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
+    def forward(self, x: torch.Tensor, y: torch.Tensor, fused: bool = True) -> torch.Tensor:
+        """fused=True: W13 and SwiGLU in one call (K split across workgroups, partials
+        summed by the SwiGLU kernel); fused=False: the reference's sequence, W13 GEMM
+        into h13 then kimi_marlin_w13_swiglu."""
         rows = x.shape[0]
-        self.up.forward(x, self.h13[:rows])
-        ops.kimi_marlin_w13_swiglu(self.h13[:rows], self.act[:rows], rows, self.I)
+        if fused and self.up.block_size <= 16:
+            if self.up._routed_rows != rows:
+                self.up.route(rows)
+            ops.wna16_w13_swiglu(self.up.gemm_ws, self.up.routing, x, self.up.w,
+                                 self.act[:rows], top_k=1, size_m=rows)
+        else:
+            self.up.forward(x, self.h13[:rows])
+            ops.kimi_marlin_w13_swiglu(self.h13[:rows], self.act[:rows], rows, self.I)
         self.down.forward(self.act[:rows], y)
         return y
 

@@ -419,6 +419,25 @@ def wna16_gemm(workspace: KimiMarlinWna16Workspace, routing: KimiMarlinRouting,
                   KIMI_K2_INT4_GROUP_SIZE, 0, _stream())
 
 
+def wna16_w13_swiglu(workspace: KimiMarlinWna16Workspace, routing: KimiMarlinRouting,
+                     input: torch.Tensor, weight: MarlinInt4Weight, act: torch.Tensor, *,
+                     top_k: int, size_m: int) -> None:
+    """act[sorted_id] = SwiGLU(bf16(A[sorted_id / top_k] . dequant(W13[expert]))) in one
+    call (small-batch decode: K split across workgroups, the partials summed by the SwiGLU
+    kernel).  The workspace's c_tmp holds the partials."""
+    inter = weight.out_dim // 2
+    _ensure(workspace.block_size == routing.block_size, "workspace / routing block size differ")
+    _ensure(2 * inter <= workspace.max_size_n, "W13 width exceeds the workspace")
+    _ensure(act.dtype == torch.bfloat16 and act.numel() >= size_m * top_k * inter,
+            "act must be bf16 [size_m * top_k, inter]")
+    _lib.call("pega_wna16_w13_swiglu", _ptr(input), _ptr(act), _ptr(workspace.c_tmp),
+              workspace.c_tmp.numel(), _ptr(weight.weight_packed_uint4b8),
+              _ptr(weight.weight_scale_permuted), _ptr(routing.sorted_token_ids),
+              _ptr(routing.expert_ids), _ptr(routing.num_tokens_post_padded),
+              routing.sorted_token_ids.numel(), routing.block_size, top_k, size_m, inter,
+              weight.in_dim, weight.local_experts, 32, 0, _stream())
+
+
 def kimi_marlin_wna16_w13_gemm(workspace, routing, input, weight, topk_weight, output_w13):
     """W13 call: top_k = routing.topk, no weight multiply, size_m = active tokens
     (experts.rs:1024-1080)."""

@@ -168,3 +168,37 @@ def test_gemm_block8_four_waves_exact(oracle):
     got, ref = _run(oracle, E=E, N=N, K=K, T=T, topk=8, bs=8, mul=False, a_bits=a_bits, q=q,
                     scale_bits=scale_bits, idx=idx, tw=np.ones((T, 8), np.float32), threads=16)
     assert np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize("E,T,topk,bs,inter,K", [(1, 1, 1, 8, 2048, 7168), (1, 8, 1, 8, 1024, 2048),
+                                                 (48, 4, 8, 16, 512, 1024)])
+def test_w13_swiglu_fused_exact(oracle, E, T, topk, bs, inter, K):
+    """pega_wna16_w13_swiglu (W13 with K split across workgroups, partials summed and
+    rounded by the SwiGLU kernel) on exact inputs: every W13 value is exact, so the
+    activations equal oracle SwiGLU(oracle W13) bit for bit; rows of routes that are
+    not local keep their contents."""
+    from pegainfer_amd import ops
+    g = np.random.default_rng(E * 100 + T)
+    N = 2 * inter
+    q = g.integers(-8, 8, size=(E, N, K))
+    scale_bits = oracle.f32_to_bf16(
+        (2.0 ** g.integers(-6, -2, size=(E, N, K // 32))).astype(np.float32))
+    a_bits = oracle.f32_to_bf16(g.integers(-2, 3, size=(T, K)).astype(np.float32))
+    idx = g.integers(0, 2 * E, size=(T, topk)).astype(np.int32)  # about half not local
+    w, packed = _setup(E, N, K, q, scale_bits)
+    ws = ops.KimiMarlinRouteWorkspace(T, bs, topk=topk, local_experts=E)
+    routing = ops.moe_align_block_size(ws, dev(idx.reshape(-1)), T, T, 0)
+    gws = ops.KimiMarlinWna16Workspace(ws.max_m_blocks, N, bs, extra_splits=16)
+    act = torch.full((T * topk, inter), 3.0, dtype=torch.bfloat16, device="cuda")
+    for _ in range(2):
+        ops.wna16_w13_swiglu(gws, routing, dev(a_bits), w, act, top_k=topk, size_m=T)
+    got = host(act)
+    r = {k: host(v) for k, v in (("sorted_token_ids", routing.sorted_token_ids),
+                                 ("expert_ids", routing.expert_ids),
+                                 ("num_tokens_post_padded", routing.num_tokens_post_padded))}
+    ref13 = oracle.wna16_gemm(a_bits, packed, scale_bits, r, np.ones((T, topk), np.float32),
+                              moe_block_size=bs, top_k=topk, mul_topk_weights=False, size_m=T,
+                              size_n=N, size_k=K, threads=16)
+    local = (idx.reshape(-1) < E)
+    assert np.array_equal(got[local], oracle.swiglu(ref13, inter)[local])
+    assert (got[~local] == 0x4040).all()  # bf16(3.0) untouched

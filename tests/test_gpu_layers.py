@@ -60,7 +60,7 @@ def test_c2_expert_ffn(oracle, b):
     ffn = layer.ExpertFFN(layer.package_w13(gate, up), layer.package_projection(*down), max_rows=8)
     x = synth.normal_bf16(synth.rng(2, 2), (b, 7168))
     y = torch.zeros(b, 7168, dtype=torch.bfloat16, device="cuda")
-    ffn.forward(dev(x), y)
+    ffn.forward(dev(x), y, fused=False)  # the reference's call sequence, stage by stage
     w13p = np.concatenate([gate[0], up[0]], axis=1)
     w13s = np.concatenate([gate[1], up[1]], axis=1)
     r_up = _routing_host(ffn.up.routing)
@@ -81,6 +81,12 @@ def test_c2_expert_ffn(oracle, b):
                             np.ones(b, np.float32), moe_block_size=8, top_k=1,
                             mul_topk_weights=False, size_m=b, size_n=7168, size_k=2048, threads=8)
     assert_bf16_close(host(y), e2e, rtol=2e-2, atol=2e-3, what="C2 end to end")
+    # the fused W13 + SwiGLU path (split K, partials summed by the SwiGLU kernel)
+    y_fused = torch.zeros_like(y)
+    ffn.forward(dev(x), y_fused, fused=True)
+    assert_bf16_close(host(ffn.act[:b]), oracle.swiglu(ref13, 2048), rtol=2e-2, atol=2e-3,
+                      what="C2 fused SwiGLU")
+    assert_bf16_close(host(y_fused), e2e, rtol=2e-2, atol=2e-3, what="C2 fused end to end")
 
 
 def test_c3_kimi_decode_layer(oracle):
