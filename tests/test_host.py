@@ -115,6 +115,28 @@ def test_repack_and_elementwise_reject_bad_arguments():
     assert _call("pega_kimi_router_select", FAKE, FAKE, FAKE, FAKE, 4, 384, 400,
                  ctypes.c_float(1.0), NULL)[0] == 1
     assert _call("pega_dsv2_router_select", FAKE, FAKE, FAKE, 4, 64, 0, NULL)[0] == 1
+    # local-route combine: hidden % 8 and experts > 0 required
+    assert _call("pega_moe_combine_local_f32", FAKE, FAKE, NULL, FAKE, 4, 8, 100, 0, 48,
+                 NULL)[0] == 1
+    assert _call("pega_moe_combine_local_f32", FAKE, FAKE, NULL, FAKE, 4, 8, 7168, 0, 0,
+                 NULL)[0] == 1
+
+
+def test_fused_w13_swiglu_rejects_bad_arguments():
+    def call(**kw):
+        base = dict(partials_len=1 << 20, sorted_len=15, bs=8, top_k=1, m=1, inter=2048, k=7168,
+                    experts=1, group=32, partials=FAKE)
+        base.update(kw)
+        return _call("pega_wna16_w13_swiglu", FAKE, FAKE, base["partials"],
+                     ctypes.c_longlong(base["partials_len"]), FAKE, FAKE, FAKE, FAKE, FAKE,
+                     base["sorted_len"], base["bs"], base["top_k"], base["m"], base["inter"],
+                     base["k"], base["experts"], base["group"], 0, NULL)
+    assert call(bs=64)[0] == 1             # the fused path is for decode block sizes
+    assert call(group=64)[0] == 1
+    assert call(partials=NULL)[0] == 1
+    rc, msg = call(partials_len=100)
+    assert rc == 1 and "partials" in msg  # fewer floats than one share needs
+    assert call(inter=2000)[0] == 801      # width must be a multiple of 64
 
 
 # ------------------------------------------------------------- Python mirror logic
