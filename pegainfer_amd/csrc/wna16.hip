@@ -558,33 +558,76 @@ __device__ __forceinline__ void prefill_tile(const GemmArgs& p, PfStage* s_a, ui
   }
 }
 
+// The tiles of one launch: every m-block whose position in its expert's run of
+// blocks is a multiple of the blocks-per-tile count starts a tile.  Workgroup
+// row y takes the y-th such block in block order, found by a ballot scan of
+// the block experts, so the grid holds the tiles first and the rows past the
+// last tile at its end.  (Rows indexed by m-block instead leave an idle
+// workgroup after every leader in dispatch order, and the round-robin spread
+// over shader engines then puts all the work on half of them.)
+constexpr int kPfScanSlab = 1024;  // block experts staged in LDS per scan pass
+
 __global__ __launch_bounds__(256, 2) void wna16_prefill_kernel(GemmArgs p) {
   __shared__ __align__(16) PfStage s_a[2];
   __shared__ __align__(16) uint32_t s_w[4][kSlotDwords];
   __shared__ int s_sid[kPfRows];
-  __shared__ int s_seg_break;
+  __shared__ int s_e[kPfScanSlab];
+  __shared__ int s_tile;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int mb = blockIdx.y;
+  const int ty = blockIdx.y;
   int ntp = p.ntp[0];
   if (ntp > p.sorted_len) ntp = p.sorted_len;
   const int nblocks = ntp / p.bs;
-  if (mb >= nblocks) return;
-  const int expert = __builtin_amdgcn_readfirstlane(p.expert_ids[mb]);
-  if (expert < 0 || expert >= p.num_experts) return;
-
-  // Start of this expert's run of blocks: 1 + the last j < mb whose expert differs.
-  if (tid == 0) s_seg_break = -1;
-  __syncthreads();
-  for (int j = tid; j < mb; j += blockDim.x)
-    if (p.expert_ids[j] != expert) atomicMax(&s_seg_break, j);
-  __syncthreads();
-  const int seg_start = s_seg_break + 1;
+  if (ty >= nblocks) return;  // a tile starts at a distinct block
   const int per_tile = kPfRows / p.bs;  // m-blocks per 128-row tile (>= 1)
-  if ((mb - seg_start) % per_tile != 0) return;
-  int nb = 1;
-  while (nb < per_tile && mb + nb < nblocks && p.expert_ids[mb + nb] == expert) ++nb;
+
+  // Wave 0 carries the scan state across 64-block windows and slabs.
+  int tiles_before = 0;   // tiles starting before the current window
+  int run_start = 0;      // first block of the run the window starts in
+  int prev_e = -1;        // expert of the block before the window (none at block 0)
+  int mb = -1;
+  for (int b0 = 0; b0 < nblocks; b0 += kPfScanSlab) {
+    const int n = min(kPfScanSlab, nblocks - b0);
+    __syncthreads();  // the previous slab is no longer read
+    for (int i = tid; i < n; i += blockDim.x) s_e[i] = p.expert_ids[b0 + i];
+    if (tid == 0) s_tile = -1;
+    __syncthreads();
+    if (wave == 0) {
+      for (int w0 = 0; w0 < n; w0 += 64) {
+        const int i = w0 + lane;
+        const int blk = b0 + i;
+        const bool in = i < n;
+        const int e = in ? s_e[i] : -1;
+        const int ep = i > w0 ? s_e[i - 1] : prev_e;
+        const uint64_t starts = __ballot(in && (blk == 0 || e != ep));
+        const uint64_t upto = starts & ((2ull << lane) - 1ull);
+        const int run = upto ? b0 + w0 + 63 - __builtin_clzll(upto) : run_start;
+        const bool lead = in && e >= 0 && e < p.num_experts && (blk - run) % per_tile == 0;
+        uint64_t leads = __ballot(lead);
+        const int cnt = __builtin_popcountll(leads);
+        if (ty - tiles_before < cnt) {
+          for (int k = ty - tiles_before; k > 0; --k) leads &= leads - 1ull;
+          if (lane == 0) s_tile = b0 + w0 + __builtin_ctzll(leads);
+          break;
+        }
+        tiles_before += cnt;
+        if (starts) run_start = b0 + w0 + 63 - __builtin_clzll(starts);
+        prev_e = s_e[min(w0 + 63, n - 1)];
+      }
+    }
+    __syncthreads();
+    mb = s_tile;
+    if (mb >= 0) break;
+  }
+  if (mb < 0) return;  // past the last tile
+  const int expert = __builtin_amdgcn_readfirstlane(p.expert_ids[mb]);
+  // blocks of this tile: up to per_tile, while the expert stays the same
+  const bool same = lane > 0 && lane < per_tile && mb + lane < nblocks &&
+                    p.expert_ids[mb + lane] == expert;
+  const uint64_t differ = ~__ballot(same) & ~1ull;  // bit 0: the leader itself
+  const int nb = min(per_tile, static_cast<int>(__builtin_ctzll(differ)));
   const int rows = nb * p.bs;
 
   const int valid_limit = p.size_m * p.top_k;

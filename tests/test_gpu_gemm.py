@@ -202,3 +202,64 @@ def test_w13_swiglu_fused_exact(oracle, E, T, topk, bs, inter, K):
     local = (idx.reshape(-1) < E)
     assert np.array_equal(got[local], oracle.swiglu(ref13, inter)[local])
     assert (got[~local] == 0x4040).all()  # bf16(3.0) untouched
+
+
+def test_prefill_tile_scan_runs_and_gaps(oracle):
+    """Prefill tiles found by the block-expert scan: an expert with two separate
+    runs, runs shorter and longer than a tile, and blocks of expert -1 holding
+    real token ids (their rows must stay untouched)."""
+    from types import SimpleNamespace
+    from pegainfer_amd import ops
+    g = np.random.default_rng(11)
+    E, N, K, bs = 3, 128, 256, 32  # 32-row blocks: prefill kernel, 4 blocks per tile
+    runs = [(0, 3), (-1, 1), (1, 5), (0, 2), (2, 1), (-1, 2), (1, 4)]
+    nblocks = sum(n for _, n in runs)
+    T = nblocks * bs
+    expert_ids, sorted_ids, tok = [], [], 0
+    for e, n in runs:
+        for b in range(n):
+            expert_ids.append(e)
+            for r in range(bs):
+                if e >= 0 and b == n - 1 and r >= bs - 5:
+                    sorted_ids.append(T)  # padding at the end of a run
+                else:
+                    sorted_ids.append(tok)
+                    tok += 1
+    q = g.integers(-8, 8, size=(E, N, K))
+    scale_bits = oracle.f32_to_bf16(np.ldexp(1.0, g.integers(-6, 2, size=(E, N, K // 32))).astype(np.float32))
+    a_bits = oracle.f32_to_bf16(g.integers(-4, 5, size=(T, K)).astype(np.float32))
+    w, packed = _setup(E, N, K, q, scale_bits)
+    st, ei = np.array(sorted_ids, np.int32), np.array(expert_ids, np.int32)
+    ntp = np.array([nblocks * bs], np.int32)
+    routing = SimpleNamespace(block_size=bs, max_m_blocks=nblocks, max_padded_tokens=nblocks * bs,
+                              sorted_token_ids=dev(st), expert_ids=dev(ei),
+                              num_tokens_post_padded=dev(ntp))
+    gws = ops.KimiMarlinWna16Workspace(nblocks, N, bs)
+    out = torch.full((T, N), 7.0, dtype=torch.bfloat16, device="cuda")
+    tw = np.ones((T, 1), np.float32)
+    ops.wna16_gemm(gws, routing, dev(a_bits), w, dev(tw.reshape(-1)), out, top_k=1,
+                   mul_topk_weights=False, size_m=T)
+    got = host(out)
+    ref = oracle.wna16_gemm(a_bits, packed, scale_bits,
+                            {"sorted_token_ids": st, "expert_ids": ei, "num_tokens_post_padded": ntp},
+                            tw, moe_block_size=bs, top_k=1, mul_topk_weights=False, size_m=T,
+                            size_n=N, size_k=K, output=np.full((T, N), 0x40E0, np.uint16), threads=8)
+    assert np.array_equal(got, ref)
+    gap_rows = [sorted_ids[b * bs + r] for b, e in enumerate(expert_ids) if e < 0 for r in range(bs)]
+    assert (got[gap_rows] == 0x40E0).all(), "rows of expert -1 blocks must stay untouched"
+
+
+def test_prefill_tile_scan_over_many_blocks(oracle):
+    """More than 1024 m-blocks: the tile scan stages the block experts in
+    several passes."""
+    g = np.random.default_rng(12)
+    E, N, K, T, topk, bs = 8, 64, 64, 4400, 8, 32
+    q = g.integers(-8, 8, size=(E, N, K))
+    scale_bits = oracle.f32_to_bf16(np.ldexp(1.0, g.integers(-6, 2, size=(E, N, K // 32))).astype(np.float32))
+    a_bits = oracle.f32_to_bf16(g.integers(-4, 5, size=(T, K)).astype(np.float32))
+    idx = np.stack([g.permutation(E) for _ in range(T)]).astype(np.int32)  # every token to every expert
+    got, ref = _run(oracle, E=E, N=N, K=K, T=T, topk=topk, bs=bs, mul=False, a_bits=a_bits, q=q,
+                    scale_bits=scale_bits, idx=idx, tw=np.ones((T, topk), np.float32))
+    routes = int((idx < E).sum())
+    assert routes // bs > 1024, "the case must span more than one scan slab"
+    assert np.array_equal(got, ref)
