@@ -124,14 +124,18 @@ int pega_wna16_gemm(const uint16_t* input, uint16_t* output, float* c_tmp, long 
                     bool mul_topk_weights, int size_m, int size_n, int size_k, int local_experts,
                     int group_size, int sm_count, hipStream_t stream);
 
-/* No reference counterpart: W13 GEMM fused with SwiGLU for the small-batch decode path
- * (block size 8 or 16; one expert at batch 1-8 is the case it is for).  The reference runs
- * kimi_marlin_wna16_gemm_cuda (W13, top_k rows) then kimi_marlin_w13_swiglu_cuda.  Here K is
- * split across workgroups so that a handful of (block, tile) units still fill the GPU; the
- * fp32 partials (partials: >= size_m * top_k * 2 * intermediate_dim floats, more allows more
- * shares) are summed in share order by the SwiGLU kernel, which rounds gate and up to bf16
- * exactly as the W13 output is rounded.  act = [size_m * top_k, intermediate_dim] bf16, rows
- * of routes not listed in sorted_token_ids are left as they are. */
+/* No reference counterpart: W13 GEMM fused with SwiGLU.  The reference runs
+ * kimi_marlin_wna16_gemm_cuda (W13, top_k rows) then kimi_marlin_w13_swiglu_cuda over every
+ * route row; here act = [size_m * top_k, intermediate_dim] bf16 gets the same bits for the
+ * routed rows only (other rows are left as they are), and the W13 output never reaches HBM.
+ *  - Block size 8 or 16 (decode; one expert at batch 1-8 is the case it is for): K is split
+ *    across workgroups so that a handful of (block, tile) units still fill the GPU; the fp32
+ *    partials (partials: >= size_m * top_k * 2 * intermediate_dim floats, more allows more
+ *    shares) are summed in share order by the SwiGLU kernel, which rounds gate and up to bf16
+ *    exactly as the W13 output is rounded.
+ *  - Block size 32, 48 or 64 (prefill): the 128-row tile GEMM takes each gate tile and its up
+ *    tile in one workgroup and applies SwiGLU in its epilogue; partials is not used (may be
+ *    NULL, partials_len 0). */
 int pega_wna16_w13_swiglu(const uint16_t* input, uint16_t* act, float* partials,
                           long long partials_len, const uint8_t* b_qweight,
                           const uint16_t* b_scales, const int32_t* sorted_token_ids,

@@ -153,6 +153,8 @@ struct GemmArgs {
   int splits;       // decode: K split across `splits` workgroups (partial != nullptr)
   float* partial;   // non-null: fp32 partial sums [splits][size_m * top_k][size_n]
                     // instead of the bf16 output (finished by the consumer kernel)
+  uint16_t* act;    // prefill, non-null: W13 + SwiGLU, act[sid][inter] instead of the output
+  int inter;        // with act: gate columns [0, inter), up columns [inter, 2 inter)
 };
 
 __device__ __forceinline__ uint16_t epilogue_value(float acc, int sid, const GemmArgs& p) {
@@ -541,6 +543,66 @@ __device__ __forceinline__ void prefill_tile(const GemmArgs& p, PfStage* s_a, ui
     __syncthreads();
   }
 
+  if (p.act != nullptr) {
+    // W13 + SwiGLU in two row halves (rows 64 ph .. 64 ph + 63, the 32-row
+    // blocks 2 ph and 2 ph + 1): the gate and up waves of both tile pairs put
+    // their bf16 values into the activation stages (free since the loop's last
+    // barrier) as [pair][64 rows][65] words, gate in the low half and up in the
+    // high half; then each thread finishes half a row of one pair (32 columns,
+    // four 16-byte stores).  Every wave passes the same four barriers whatever
+    // its routed-block count.
+    constexpr int kXStride = 65;  // words per row (odd: the two k-halves' rows use other banks)
+    uint16_t* x16 = reinterpret_cast<uint16_t*>(s_a);
+    const uint32_t* x32 = reinterpret_cast<const uint32_t*>(s_a);
+    const int wave = threadIdx.x >> 6;
+    const int g0 = blockIdx.x * 2;  // first gate tile of this workgroup
+    const int gate_tiles = p.inter >> 6;
+#pragma unroll
+    for (int ph = 0; ph < 2; ++ph) {
+      if constexpr (RB > 0) {
+        const int pair = wave & 1, half = wave >> 1;  // half 0: gate, 1: up
+        const int col = (c >> 3) * 16 + (c & 7);
+#pragma unroll
+        for (int rbl = 0; rbl < 2; ++rbl) {
+          const int rb = 2 * ph + rbl;
+          if (rb < RB) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+              const int row = 32 * rbl + acc_row(i, h);
+              uint16_t* x = x16 + ((pair * 64 + row) * kXStride + col) * 2 + half;
+              x[0] = f2bf(accx[rb < NACC ? rb : 0][i]);
+              x[16] = f2bf(accy[rb < NACC ? rb : 0][i]);  // column col + 8
+            }
+          }
+        }
+      }
+      __syncthreads();
+      const int pair_t = threadIdx.x >> 7, r = (threadIdx.x >> 1) & 63, part = threadIdx.x & 1;
+      const int sid = s_sid[64 * ph + r];
+      if (g0 + pair_t < gate_tiles &&
+          static_cast<unsigned>(sid) < static_cast<unsigned>(valid_limit)) {
+        const uint32_t* src = x32 + (pair_t * 64 + r) * kXStride + 32 * part;
+        uint16_t* dst =
+            p.act + static_cast<long long>(sid) * p.inter + (g0 + pair_t) * 64 + 32 * part;
+#pragma unroll 1
+        for (int q = 0; q < 4; ++q) {
+          uint32_t w[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t v0 = src[8 * q + 2 * e], v1 = src[8 * q + 2 * e + 1];
+            const uint16_t lo = swiglu_one(bf2f(static_cast<uint16_t>(v0 & 0xffffu)),
+                                           bf2f(static_cast<uint16_t>(v0 >> 16)));
+            const uint16_t hi = swiglu_one(bf2f(static_cast<uint16_t>(v1 & 0xffffu)),
+                                           bf2f(static_cast<uint16_t>(v1 >> 16)));
+            w[e] = static_cast<uint32_t>(lo) | (static_cast<uint32_t>(hi) << 16);
+          }
+          *reinterpret_cast<uint4*>(dst + 8 * q) = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+      }
+      __syncthreads();  // the next half reuses the stages
+    }
+    return;
+  }
   if constexpr (RB > 0) {
     const int n0 = nt * 64 + (c >> 3) * 16 + (c & 7);
 #pragma unroll
@@ -642,8 +704,19 @@ __global__ __launch_bounds__(256, 2) void wna16_prefill_kernel(GemmArgs p) {
   const uint64_t hi_rows = __ballot(s_sid[64 + lane] < valid_limit);
   const int row_end = hi_rows ? 128 - __builtin_clzll(hi_rows)
                               : (lo_rows ? 64 - __builtin_clzll(lo_rows) : 0);
-  const int nt = blockIdx.x * 4 + wave;
-  const int rb = (nt < (p.size_n >> 6)) ? __builtin_amdgcn_readfirstlane((row_end + 31) >> 5) : 0;
+  // Column tiles of the four waves: four consecutive tiles, or with SwiGLU two
+  // gate tiles (waves 0, 1) and their up tiles (waves 2, 3).
+  int nt;
+  bool tile_ok;
+  if (p.act != nullptr) {
+    const int gate = blockIdx.x * 2 + (wave & 1);
+    tile_ok = gate < (p.inter >> 6);
+    nt = wave < 2 ? gate : gate + (p.inter >> 6);
+  } else {
+    nt = blockIdx.x * 4 + wave;
+    tile_ok = nt < (p.size_n >> 6);
+  }
+  const int rb = tile_ok ? __builtin_amdgcn_readfirstlane((row_end + 31) >> 5) : 0;
   uint32_t* s_w_wave = s_w[wave];
   switch (rb) {
     case 0: prefill_tile<0>(p, s_a, s_w_wave, s_sid, expert, nt); break;
@@ -768,14 +841,15 @@ int wna16_w13_swiglu(const uint16_t* input, uint16_t* act, float* partials, long
                      const int32_t* num_tokens_post_padded, int sorted_token_ids_len,
                      int moe_block_size, int top_k, int size_m, int inter, int size_k,
                      int local_experts, int group_size, int cu_count, hipStream_t stream) {
-  if (!input || !act || !partials || !b_qweight || !b_scales || !sorted_token_ids ||
-      !expert_ids || !num_tokens_post_padded)
+  if (!input || !act || !b_qweight || !b_scales || !sorted_token_ids || !expert_ids ||
+      !num_tokens_post_padded)
     return fail(kInvalidValue, "w13_swiglu: null pointer");
   if (group_size != 32 || top_k <= 0 || size_m <= 0 || inter <= 0 || size_k <= 0 ||
       sorted_token_ids_len <= 0 || local_experts <= 0)
     return fail(kInvalidValue, "w13_swiglu: bad shape m=%d inter=%d k=%d", size_m, inter, size_k);
-  if (moe_block_size != 8 && moe_block_size != 16)
-    return fail(kInvalidValue, "w13_swiglu: block size %d not in {8, 16}", moe_block_size);
+  if (!valid_block_size(moe_block_size))
+    return fail(kInvalidValue, "w13_swiglu: block size %d not in {8, 16, 32, 48, 64}",
+                moe_block_size);
   const int size_n = 2 * inter;
   if (size_k % 64 != 0 || inter % 64 != 0)
     return fail(kNotSupported, "w13_swiglu: size_k %% 64 and inter %% 64 must be 0");
@@ -783,6 +857,19 @@ int wna16_w13_swiglu(const uint16_t* input, uint16_t* act, float* partials, long
       (reinterpret_cast<uintptr_t>(act) & 15u) != 0 ||
       (reinterpret_cast<uintptr_t>(partials) & 15u) != 0)
     return fail(kInvalidValue, "w13_swiglu: input, act and partials must be 16-byte aligned");
+  const int max_m_blocks = ceil_div(sorted_token_ids_len, moe_block_size);
+  if (max_m_blocks > 65535) return fail(kNotSupported, "w13_swiglu: too many m-blocks");
+  if (moe_block_size > 16) {
+    // Prefill: the tile GEMM with the SwiGLU epilogue (partials not used).
+    GemmArgs args{input, nullptr, nullptr, reinterpret_cast<const uint32_t*>(b_qweight),
+                  b_scales, nullptr, sorted_token_ids, expert_ids, num_tokens_post_padded,
+                  nullptr, sorted_token_ids_len, moe_block_size, top_k, 0, size_m, size_n,
+                  size_k, local_experts, 1, nullptr, act, inter};
+    hipLaunchKernelGGL(wna16_prefill_kernel, dim3(ceil_div(inter / 64, 2), max_m_blocks),
+                       dim3(256), 0, stream, args);
+    return launch_status("w13_swiglu (prefill)");
+  }
+  if (!partials) return fail(kInvalidValue, "w13_swiglu: partials required for block sizes 8, 16");
   const long long routes = static_cast<long long>(size_m) * top_k;
   if (partials_len < routes * size_n)
     return fail(kInvalidValue, "w13_swiglu: partials holds %lld floats, needs >= %lld",
@@ -790,8 +877,6 @@ int wna16_w13_swiglu(const uint16_t* input, uint16_t* act, float* partials, long
   if (cu_count <= 0) cu_count = current_cu_count();
   if (cu_count <= 0) return fail(kInvalidValue, "w13_swiglu: no device");
 
-  const int max_m_blocks = ceil_div(sorted_token_ids_len, moe_block_size);
-  if (max_m_blocks > 65535) return fail(kNotSupported, "w13_swiglu: too many m-blocks");
   const int n_tiles = size_n / 64;
   const int groups = size_k / 32;
   const long long est_blocks = routes < max_m_blocks ? routes : max_m_blocks;

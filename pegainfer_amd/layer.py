@@ -71,7 +71,8 @@ class RoutedExperts:
                 out_f32: torch.Tensor, combine: str = "sum", w13_timer=None,
                 reference_flow: bool = False) -> torch.Tensor:
         """Routed-expert forward (moe_nccl.rs:152-203 order: align, W13, SwiGLU, W2
-        with the top-k weight, top-k combine).
+        with the top-k weight, top-k combine).  With prefill block sizes (> 16) W13
+        and SwiGLU are one call unless reference_flow is set.
 
         combine "sum": the weight is applied in the W2 epilogue and rows are summed
         (Kimi); "weighted": W2 without weight and an fmaf-chain combine (DSV2).
@@ -91,11 +92,18 @@ class RoutedExperts:
         if reference_flow:
             w13_out.zero_()
         mark = w13_timer.start() if w13_timer is not None else None
-        ops.wna16_gemm(self.gemm_ws, routing, hidden, self.w13, topk_w, w13_out, top_k=self.topk,
-                       mul_topk_weights=False, size_m=T)
-        if w13_timer is not None:
-            w13_timer.stop(mark)
-        ops.kimi_marlin_w13_swiglu(w13_out, act, rows, self.I)
+        if not reference_flow and routing.block_size > 16:
+            # prefill: SwiGLU in the W13 tile epilogue, routed rows only (same bits)
+            ops.wna16_w13_swiglu(self.gemm_ws, routing, hidden, self.w13, act, top_k=self.topk,
+                                 size_m=T)
+            if w13_timer is not None:
+                w13_timer.stop(mark)
+        else:
+            ops.wna16_gemm(self.gemm_ws, routing, hidden, self.w13, topk_w, w13_out,
+                           top_k=self.topk, mul_topk_weights=False, size_m=T)
+            if w13_timer is not None:
+                w13_timer.stop(mark)
+            ops.kimi_marlin_w13_swiglu(w13_out, act, rows, self.I)
         weighted_in_gemm = combine == "sum"
         if reference_flow:
             route_out.zero_()
@@ -157,11 +165,12 @@ class ExpertFFN:
         self.act = torch.zeros(max_rows, self.I, **bf)
 
     def forward(self, x: torch.Tensor, y: torch.Tensor, fused: bool = True) -> torch.Tensor:
-        """fused=True: W13 and SwiGLU in one call (K split across workgroups, partials
-        summed by the SwiGLU kernel); fused=False: the reference's sequence, W13 GEMM
-        into h13 then kimi_marlin_w13_swiglu."""
+        """fused=True: W13 and SwiGLU in one call (block sizes 8/16: K split across
+        workgroups, partials summed by the SwiGLU kernel; larger: SwiGLU in the tile
+        GEMM's epilogue); fused=False: the reference's sequence, W13 GEMM into h13
+        then kimi_marlin_w13_swiglu."""
         rows = x.shape[0]
-        if fused and self.up.block_size <= 16:
+        if fused:
             if self.up._routed_rows != rows:
                 self.up.route(rows)
             ops.wna16_w13_swiglu(self.up.gemm_ws, self.up.routing, x, self.up.w,

@@ -423,8 +423,9 @@ def wna16_w13_swiglu(workspace: KimiMarlinWna16Workspace, routing: KimiMarlinRou
                      input: torch.Tensor, weight: MarlinInt4Weight, act: torch.Tensor, *,
                      top_k: int, size_m: int) -> None:
     """act[sorted_id] = SwiGLU(bf16(A[sorted_id / top_k] . dequant(W13[expert]))) in one
-    call (small-batch decode: K split across workgroups, the partials summed by the SwiGLU
-    kernel).  The workspace's c_tmp holds the partials."""
+    call, routed rows only.  Block sizes 8/16: K split across workgroups, the partials (the
+    workspace's c_tmp) summed by the SwiGLU kernel; 32/48/64: the tile GEMM with a SwiGLU
+    epilogue."""
     inter = weight.out_dim // 2
     _ensure(workspace.block_size == routing.block_size, "workspace / routing block size differ")
     _ensure(2 * inter <= workspace.max_size_n, "W13 width exceeds the workspace")

@@ -171,12 +171,16 @@ def test_gemm_block8_four_waves_exact(oracle):
 
 
 @pytest.mark.parametrize("E,T,topk,bs,inter,K", [(1, 1, 1, 8, 2048, 7168), (1, 8, 1, 8, 1024, 2048),
-                                                 (48, 4, 8, 16, 512, 1024)])
+                                                 (48, 4, 8, 16, 512, 1024),
+                                                 (3, 300, 4, 32, 192, 256),
+                                                 (48, 160, 8, 48, 1024, 512),
+                                                 (4, 512, 2, 64, 1408, 256)])
 def test_w13_swiglu_fused_exact(oracle, E, T, topk, bs, inter, K):
-    """pega_wna16_w13_swiglu (W13 with K split across workgroups, partials summed and
-    rounded by the SwiGLU kernel) on exact inputs: every W13 value is exact, so the
+    """pega_wna16_w13_swiglu on exact inputs: every W13 value is exact, so the
     activations equal oracle SwiGLU(oracle W13) bit for bit; rows of routes that are
-    not local keep their contents."""
+    not local keep their contents.  Block sizes 8/16 take the split-K path (partials
+    summed and rounded by the SwiGLU kernel), 32/48/64 the tile GEMM with the SwiGLU
+    epilogue (an odd gate-tile count leaves a workgroup half its columns)."""
     from pegainfer_amd import ops
     g = np.random.default_rng(E * 100 + T)
     N = 2 * inter

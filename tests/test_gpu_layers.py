@@ -39,6 +39,17 @@ def _routed_layer(gate, up, down, *, tokens, topk, block_size, global_start=0):
                                global_start=global_start)
 
 
+def _unfused_w13(routed, hidden_dev, topk_w_dev, T):
+    """The W13 GEMM alone (bf16 output) with the layer's routing, into a zeroed
+    buffer.  The prefill layer fuses SwiGLU into W13, so its activations must be
+    SwiGLU of exactly these bits."""
+    from pegainfer_amd import ops
+    out = torch.zeros(T * routed.topk, 2 * routed.I, dtype=torch.bfloat16, device="cuda")
+    ops.wna16_gemm(routed.gemm_ws, routed.routing, hidden_dev, routed.w13, topk_w_dev, out,
+                   top_k=routed.topk, mul_topk_weights=False, size_m=T)
+    return host(out)
+
+
 def test_c1_dense_gemv(oracle):
     from pegainfer_amd import layer, synth
     g = synth.rng(1, 1)
@@ -155,14 +166,15 @@ def test_c4_dsv2_layer(oracle):
     shared = layer.ExpertFFN(layer.package_w13(sg, su), layer.package_projection(*sd), max_rows=T)
     moe = layer.Dsv2MoeLayer(routed, shared)
     out = torch.zeros(T, H, dtype=torch.bfloat16, device="cuda")
-    moe.forward(dev(hidden), dev(logits), out)
+    hidden_d = dev(hidden)
+    moe.forward(hidden_d, dev(logits), out)
 
     ref_idx, ref_w = oracle.dsv2_router(logits, topk)
     assert np.array_equal(host(moe.topk_idx), ref_idx) and np.array_equal(host(moe.topk_w), ref_w)
     routing = _routing_host(routed.routing)
     w13p = np.concatenate([gate[0], up[0]], axis=1)
     w13s = np.concatenate([gate[1], up[1]], axis=1)
-    g13 = host(routed.w13_out[:T * topk])
+    g13 = _unfused_w13(routed, hidden_d, moe.topk_w, T)
     ref13 = oracle.wna16_gemm(hidden, w13p, w13s, routing, ref_w, moe_block_size=bs, top_k=topk,
                               mul_topk_weights=False, size_m=T, size_n=2 * I, size_k=H, threads=16)
     assert_bf16_close(g13, ref13, what="C4 W13")
@@ -188,7 +200,8 @@ def test_c5_kimi_prefill_sampled(oracle):
     bs = ops.kimi_marlin_block_size(T)
     moe = _routed_layer(gate, up, down, tokens=T, topk=8, block_size=bs)
     out = torch.zeros(T, H, dtype=torch.float32, device="cuda")
-    moe.forward(dev(hidden), dev(idx), dev(w), out)
+    hidden_d, w_d = dev(hidden), dev(w)
+    moe.forward(hidden_d, dev(idx), w_d, out)
     routing = _routing_host(moe.routing)
     ref_r = oracle.align_block_size(idx.reshape(-1), 0, E, bs)
     for k in ("sorted_token_ids", "expert_ids", "num_tokens_post_padded"):
@@ -207,7 +220,7 @@ def test_c5_kimi_prefill_sampled(oracle):
     rows = rows[rows < T * 8]
     w13p = np.concatenate([gate[0], up[0]], axis=1)
     w13s = np.concatenate([gate[1], up[1]], axis=1)
-    g13 = host(moe.w13_out[:T * 8])
+    g13 = _unfused_w13(moe, hidden_d, w_d, T)
     ref13 = oracle.wna16_gemm(hidden, w13p, w13s, masked, w, moe_block_size=bs, top_k=8,
                               mul_topk_weights=False, size_m=T, size_n=2 * I, size_k=H, threads=16)
     assert_bf16_close(g13[rows], ref13[rows], what="C5 W13 sampled blocks")
@@ -221,6 +234,7 @@ def test_c5_kimi_prefill_sampled(oracle):
     # (this layer's buffers start at zero); the combine is the exact fp32 sum of
     # the routed rows
     local = (idx.reshape(-1) < E)
-    assert (ro[~local] == 0).all() and (g13[~local] == 0).all()
+    assert (ro[~local] == 0).all() and (g13[~local] == 0).all() and (act[~local] == 0).all()
+    assert np.array_equal(act[local], oracle.swiglu(g13[local], I))
     assert (np.abs((ro[local].astype(np.uint32) << 16).view(np.float32)).sum(axis=1) > 0).all()
     assert np.array_equal(host(out), oracle.sum_topk_rows(ro, T, 8, H))

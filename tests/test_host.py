@@ -131,7 +131,7 @@ def test_fused_w13_swiglu_rejects_bad_arguments():
                      ctypes.c_longlong(base["partials_len"]), FAKE, FAKE, FAKE, FAKE, FAKE,
                      base["sorted_len"], base["bs"], base["top_k"], base["m"], base["inter"],
                      base["k"], base["experts"], base["group"], 0, NULL)
-    assert call(bs=64)[0] == 1             # the fused path is for decode block sizes
+    assert call(bs=24)[0] == 1             # block sizes 8, 16, 32, 48, 64 only
     assert call(group=64)[0] == 1
     assert call(partials=NULL)[0] == 1
     rc, msg = call(partials_len=100)
