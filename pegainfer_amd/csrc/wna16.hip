@@ -409,7 +409,8 @@ typedef uint16_t PfStage[kPfRows * kPfLdsStride];
 // allocates only the accumulators in use.
 template <int RB>
 __device__ __forceinline__ void prefill_tile(const GemmArgs& p, PfStage* s_a, uint32_t* s_w_wave,
-                                             const int* s_sid, int expert, int nt) {
+                                             const int* s_sid, const float* s_tw, int expert,
+                                             int nt) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int c = lane & 31, h = lane >> 5;
   const int K = p.size_k, N = p.size_n;
@@ -603,20 +604,48 @@ __device__ __forceinline__ void prefill_tile(const GemmArgs& p, PfStage* s_a, ui
     }
     return;
   }
-  if constexpr (RB > 0) {
-    const int n0 = nt * 64 + (c >> 3) * 16 + (c & 7);
+  // bf16 output (times the row's bf16 top-k weight with mul), in two row
+  // halves: the waves put their values for rows 64 ph .. 64 ph + 63 into the
+  // activation stages as [64 rows][264] bf16 (the four tiles side by side),
+  // then each thread stores one tile's 64 columns of a row with 16-byte stores.
+  constexpr int kOStride = 264;  // bf16 per row: 256 + 8, rows start on other banks
+  uint16_t* xo = reinterpret_cast<uint16_t*>(s_a);
+  const int wave = threadIdx.x >> 6;
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
+  for (int ph = 0; ph < 2; ++ph) {
+    if constexpr (RB > 0) {
+      const int col = wave * 64 + (c >> 3) * 16 + (c & 7);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int row = 32 * rb + acc_row(i, h);
-        const int sid = s_sid[row];
-        if (static_cast<unsigned>(sid) < static_cast<unsigned>(valid_limit)) {
-          p.output[static_cast<long long>(sid) * N + n0] = epilogue_value(accx[rb][i], sid, p);
-          p.output[static_cast<long long>(sid) * N + n0 + 8] = epilogue_value(accy[rb][i], sid, p);
+      for (int rbl = 0; rbl < 2; ++rbl) {
+        const int rb = 2 * ph + rbl;
+        if (rb < RB) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int row = 32 * rbl + acc_row(i, h);
+            uint16_t vx = f2bf(accx[rb < NACC ? rb : 0][i]);
+            uint16_t vy = f2bf(accy[rb < NACC ? rb : 0][i]);
+            if (p.mul) {
+              const float w = s_tw[64 * ph + row];
+              vx = f2bf(bf2f(vx) * w);
+              vy = f2bf(bf2f(vy) * w);
+            }
+            xo[row * kOStride + col] = vx;
+            xo[row * kOStride + col + 8] = vy;
+          }
         }
       }
     }
+    __syncthreads();
+    const int r = threadIdx.x >> 2, t4 = threadIdx.x & 3;
+    const int sid = s_sid[64 * ph + r];
+    const int nt_t = blockIdx.x * 4 + t4;
+    if (nt_t < (N >> 6) && static_cast<unsigned>(sid) < static_cast<unsigned>(valid_limit)) {
+      const uint4* src = reinterpret_cast<const uint4*>(xo + r * kOStride + t4 * 64);
+      uint4* dst = reinterpret_cast<uint4*>(p.output + static_cast<long long>(sid) * N + nt_t * 64);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) dst[q] = src[q];
+    }
+    __syncthreads();  // the next half reuses the stages
   }
 }
 
@@ -633,6 +662,7 @@ __global__ __launch_bounds__(256, 2) void wna16_prefill_kernel(GemmArgs p) {
   __shared__ __align__(16) PfStage s_a[2];
   __shared__ __align__(16) uint32_t s_w[4][kSlotDwords];
   __shared__ int s_sid[kPfRows];
+  __shared__ float s_tw[kPfRows];  // with mul: the row's top-k weight rounded to bf16
   __shared__ int s_e[kPfScanSlab];
   __shared__ int s_tile;
 
@@ -693,8 +723,13 @@ __global__ __launch_bounds__(256, 2) void wna16_prefill_kernel(GemmArgs p) {
   const int rows = nb * p.bs;
 
   const int valid_limit = p.size_m * p.top_k;
-  for (int r = tid; r < kPfRows; r += blockDim.x)
-    s_sid[r] = (r < rows) ? p.sorted_ids[mb * p.bs + r] : valid_limit;
+  for (int r = tid; r < kPfRows; r += blockDim.x) {
+    const int sid = (r < rows) ? p.sorted_ids[mb * p.bs + r] : valid_limit;
+    s_sid[r] = sid;
+    s_tw[r] = (p.mul && static_cast<unsigned>(sid) < static_cast<unsigned>(valid_limit))
+                  ? bf2f(f2bf(p.topk_w[sid]))
+                  : 0.0f;
+  }
   __syncthreads();
 
   // 32-row blocks past the last routed row of the tile are skipped (an
@@ -719,11 +754,11 @@ __global__ __launch_bounds__(256, 2) void wna16_prefill_kernel(GemmArgs p) {
   const int rb = tile_ok ? __builtin_amdgcn_readfirstlane((row_end + 31) >> 5) : 0;
   uint32_t* s_w_wave = s_w[wave];
   switch (rb) {
-    case 0: prefill_tile<0>(p, s_a, s_w_wave, s_sid, expert, nt); break;
-    case 1: prefill_tile<1>(p, s_a, s_w_wave, s_sid, expert, nt); break;
-    case 2: prefill_tile<2>(p, s_a, s_w_wave, s_sid, expert, nt); break;
-    case 3: prefill_tile<3>(p, s_a, s_w_wave, s_sid, expert, nt); break;
-    default: prefill_tile<4>(p, s_a, s_w_wave, s_sid, expert, nt); break;
+    case 0: prefill_tile<0>(p, s_a, s_w_wave, s_sid, s_tw, expert, nt); break;
+    case 1: prefill_tile<1>(p, s_a, s_w_wave, s_sid, s_tw, expert, nt); break;
+    case 2: prefill_tile<2>(p, s_a, s_w_wave, s_sid, s_tw, expert, nt); break;
+    case 3: prefill_tile<3>(p, s_a, s_w_wave, s_sid, s_tw, expert, nt); break;
+    default: prefill_tile<4>(p, s_a, s_w_wave, s_sid, s_tw, expert, nt); break;
   }
 }
 
@@ -795,8 +830,9 @@ int wna16_gemm(const uint16_t* input, uint16_t* output, float* c_tmp, long long 
   if (size_k % 64 != 0 || size_n % 64 != 0)
     return fail(kNotSupported, "wna16_gemm: size_k %% 64 and size_n %% 64 must be 0 (k=%d n=%d)",
                 size_k, size_n);
-  if ((reinterpret_cast<uintptr_t>(input) & 15u) != 0)
-    return fail(kInvalidValue, "wna16_gemm: input must be 16-byte aligned");
+  if ((reinterpret_cast<uintptr_t>(input) & 15u) != 0 ||
+      (reinterpret_cast<uintptr_t>(output) & 15u) != 0)
+    return fail(kInvalidValue, "wna16_gemm: input and output must be 16-byte aligned");
   if (static_cast<long long>(size_m) * top_k > 0x7fffffffLL)
     return fail(kInvalidValue, "wna16_gemm: size_m * top_k overflows int32");
   if (cu_count <= 0) cu_count = current_cu_count();

@@ -98,6 +98,10 @@ def test_gemm_rejects_reference_invalid_shapes():
     rc = f(FAKE, FAKE, NULL, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4096, 1232, 16, 8, False, 64,
            4096, 7168, 48, 32, 0, NULL)
     assert rc == 1  # c_tmp required (kimi_marlin_wna16.cu:272-274)
+    odd = ctypes.c_void_p(0x1002)
+    rc = f(FAKE, odd, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4096, 1232, 16, 8, False, 64,
+           4096, 7168, 48, 32, 0, NULL)
+    assert rc == 1  # the output rows are written with 16-byte stores
 
 
 def test_repack_and_elementwise_reject_bad_arguments():
