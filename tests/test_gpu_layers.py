@@ -189,6 +189,26 @@ def test_c4_dsv2_layer(oracle):
     assert np.array_equal(routed_f32, oracle.weighted_topk_sum(ro, ref_w, T, topk, H))
     sh = host(moe.shared_out)
     assert np.array_equal(host(out), oracle.add_f32_bf16(routed_f32, sh))
+    # the shared expert: one INT4 expert over all tokens (W13 + SwiGLU fused, then W2)
+    sI = 2 * I
+    sbs = shared.up.block_size
+    h13 = torch.zeros(T, 2 * sI, dtype=torch.bfloat16, device="cuda")
+    shared.up.forward(hidden_d, h13)  # the W13 GEMM alone, same routing
+    g13s = host(h13)
+    r_up = _routing_host(shared.up.routing)
+    ref13s = oracle.wna16_gemm(hidden, np.concatenate([sg[0], su[0]], axis=1),
+                               np.concatenate([sg[1], su[1]], axis=1), r_up,
+                               np.ones(T, np.float32), moe_block_size=sbs, top_k=1,
+                               mul_topk_weights=False, size_m=T, size_n=2 * sI, size_k=H,
+                               threads=16)
+    assert_bf16_close(g13s, ref13s, what="C4 shared W13")
+    act_s = host(shared.act[:T])
+    assert np.array_equal(act_s, oracle.swiglu(g13s, sI))
+    r_dn = _routing_host(shared.down.routing)
+    ref2s = oracle.wna16_gemm(act_s, sd[0], sd[1], r_dn, np.ones(T, np.float32),
+                              moe_block_size=sbs, top_k=1, mul_topk_weights=False, size_m=T,
+                              size_n=H, size_k=sI, threads=16)
+    assert_bf16_close(sh, ref2s, what="C4 shared W2")
 
 
 def test_c5_kimi_prefill_sampled(oracle):
