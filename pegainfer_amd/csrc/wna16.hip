@@ -778,21 +778,44 @@ __global__ void w13_swiglu_partials_kernel(GemmArgs p, uint16_t* __restrict__ ac
        idx += static_cast<long long>(gridDim.x) * blockDim.x) {
     const int pos = static_cast<int>(idx / per_row);
     const int c8 = static_cast<int>(idx - static_cast<long long>(pos) * per_row) * 8;
+    // the row's id and its block's expert go out together
     const int sid = p.sorted_ids[pos];
-    if (static_cast<unsigned>(sid) >= static_cast<unsigned>(valid_limit)) continue;
     const int e = p.expert_ids[pos / p.bs];
+    if (static_cast<unsigned>(sid) >= static_cast<unsigned>(valid_limit)) continue;
     if (e < 0 || e >= p.num_experts) continue;
     float g[8] = {0, 0, 0, 0, 0, 0, 0, 0}, u[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int sp = 0; sp < p.splits; ++sp) {
-      const float* row = p.partial + (static_cast<long long>(sp) * valid_limit + sid) * N;
-      const float4 g0 = *reinterpret_cast<const float4*>(row + c8);
-      const float4 g1 = *reinterpret_cast<const float4*>(row + c8 + 4);
-      const float4 u0 = *reinterpret_cast<const float4*>(row + inter + c8);
-      const float4 u1 = *reinterpret_cast<const float4*>(row + inter + c8 + 4);
-      g[0] += g0.x; g[1] += g0.y; g[2] += g0.z; g[3] += g0.w;
-      g[4] += g1.x; g[5] += g1.y; g[6] += g1.z; g[7] += g1.w;
-      u[0] += u0.x; u[1] += u0.y; u[2] += u0.z; u[3] += u0.w;
-      u[4] += u1.x; u[5] += u1.y; u[6] += u1.z; u[7] += u1.w;
+    const float* base = p.partial + static_cast<long long>(sid) * N + c8;
+    const long long share = static_cast<long long>(valid_limit) * N;
+    auto add = [&](const float4 (&v)[4]) {
+      g[0] += v[0].x; g[1] += v[0].y; g[2] += v[0].z; g[3] += v[0].w;
+      g[4] += v[1].x; g[5] += v[1].y; g[6] += v[1].z; g[7] += v[1].w;
+      u[0] += v[2].x; u[1] += v[2].y; u[2] += v[2].z; u[3] += v[2].w;
+      u[4] += v[3].x; u[5] += v[3].y; u[6] += v[3].z; u[7] += v[3].w;
+    };
+    auto load = [&](float4 (&v)[4], int sp) {
+      const float* row = base + sp * share;
+      v[0] = *reinterpret_cast<const float4*>(row);
+      v[1] = *reinterpret_cast<const float4*>(row + 4);
+      v[2] = *reinterpret_cast<const float4*>(row + inter);
+      v[3] = *reinterpret_cast<const float4*>(row + inter + 4);
+    };
+    // four shares' loads in flight at a time, summed in share order
+    int sp = 0;
+    for (; sp + 4 <= p.splits; sp += 4) {
+      float4 v0[4], v1[4], v2[4], v3[4];
+      load(v0, sp);
+      load(v1, sp + 1);
+      load(v2, sp + 2);
+      load(v3, sp + 3);
+      add(v0);
+      add(v1);
+      add(v2);
+      add(v3);
+    }
+    for (; sp < p.splits; ++sp) {
+      float4 v[4];
+      load(v, sp);
+      add(v);
     }
     uint32_t w[4];
 #pragma unroll
