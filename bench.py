@@ -191,7 +191,8 @@ def bench_c3(torch, args, results):
         layer_gbs=alg_bytes / (ms * 1e-3) / 1e9, w13_us=w13_ms * 1e3,
         w13_algorithmic_bytes=w13_bytes, w13_gbs=w13_bytes / (w13_ms * 1e-3) / 1e9)
     log(f"C3: layer {ms * 1e3:.1f} us graph-replayed ({results['c3']['layer_gbs']:.0f} GB/s), "
-        f"{eager_ms * 1e3:.1f} us eager; W13 {w13_ms * 1e3:.1f} us ({results['c3']['w13_gbs']:.0f} GB/s)")
+        f"{eager_ms * 1e3:.1f} us eager; W13+SwiGLU {w13_ms * 1e3:.1f} us "
+        f"({results['c3']['w13_gbs']:.0f} GB/s)")
     return dict(gate=gate, up=up, down=down, hidden=hidden_np, idx=idx,
                 w=tw.cpu().numpy(), bs=bs, alg_bytes=alg_bytes)
 
@@ -305,7 +306,7 @@ def bench_c5(torch, args, results):
                          tflops=flops / (ms * 1e-3) / 1e12, flops=flops,
                          w13_us=w13_ms * 1e3, w13_tflops=w13_flops / (w13_ms * 1e-3) / 1e12)
     log(f"C5: R={routes}, layer {ms * 1e3:.1f} us ({results['c5']['tflops']:.1f} TFLOP/s), "
-        f"W13 {w13_ms * 1e3:.1f} us ({results['c5']['w13_tflops']:.1f} TFLOP/s)")
+        f"W13+SwiGLU {w13_ms * 1e3:.1f} us ({results['c5']['w13_tflops']:.1f} TFLOP/s)")
 
 
 def load_traffic(name):
@@ -342,7 +343,7 @@ def main():
     if not args.no_cpu:
         cpu_baseline_c3(ctx, results)
     c3 = results["c3"]
-    roof = dict(bound="hbm", kernel="wna16_decode_kernel (W13, C3)",
+    roof = dict(bound="hbm", kernel="wna16_decode_kernel (W13 with SwiGLU epilogue, C3)",
                 achieved=round(c3["w13_gbs"], 1), peak=HBM_PEAK_GBS, unit="GB/s",
                 frac=round(c3["w13_gbs"] / HBM_PEAK_GBS, 4),
                 traffic=load_traffic("wna16_w13_c3"),

@@ -128,11 +128,13 @@ int pega_wna16_gemm(const uint16_t* input, uint16_t* output, float* c_tmp, long 
  * kimi_marlin_wna16_gemm_cuda (W13, top_k rows) then kimi_marlin_w13_swiglu_cuda over every
  * route row; here act = [size_m * top_k, intermediate_dim] bf16 gets the same bits for the
  * routed rows only (other rows are left as they are), and the W13 output never reaches HBM.
- *  - Block size 8 or 16 (decode; one expert at batch 1-8 is the case it is for): K is split
- *    across workgroups so that a handful of (block, tile) units still fill the GPU; the fp32
- *    partials (partials: >= size_m * top_k * 2 * intermediate_dim floats, more allows more
+ *  - Block size 8 or 16 (decode): when the (block, tile) units are too few to fill the GPU
+ *    (one expert at batch 1-8), K is split across workgroups; the fp32 partials (partials:
+ *    at least 2 * size_m * top_k * 2 * intermediate_dim floats for a split, more allows more
  *    shares) are summed in share order by the SwiGLU kernel, which rounds gate and up to bf16
- *    exactly as the W13 output is rounded.
+ *    exactly as the W13 output is rounded.  Otherwise (or when partials is NULL or too small
+ *    to split) a workgroup takes a gate tile and its up tile and applies SwiGLU in its
+ *    epilogue.
  *  - Block size 32, 48 or 64 (prefill): the 128-row tile GEMM takes each gate tile and its up
  *    tile in one workgroup and applies SwiGLU in its epilogue; partials is not used (may be
  *    NULL, partials_len 0). */

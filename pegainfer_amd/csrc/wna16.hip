@@ -217,15 +217,20 @@ struct GroupRegs {
   u32x4_t a;    // activations: row c % 16, k 16h + 8(c / 16) + 0..7
 };
 
-template <int WK, int NI, int D>
-__global__ __launch_bounds__(64 * WK, 4) void wna16_decode_kernel(GemmArgs p) {
+// kPair: W13 + SwiGLU.  The workgroup holds 2 WK waves: waves 0..WK-1 split K
+// over a gate tile, waves WK..2WK-1 over the matching up tile (inter/64 tiles
+// further), and the epilogue writes SwiGLU of the two bf16-rounded sums to
+// p.act (p.output and p.partial are not used).
+template <int WK, int NI, int D, bool kPair = false>
+__global__ __launch_bounds__(64 * WK * (kPair ? 2 : 1), 4) void wna16_decode_kernel(GemmArgs p) {
+  constexpr int kWaves = WK * (kPair ? 2 : 1);
   __shared__ int s_sid[32];
-  __shared__ float s_red[WK][2 * NI][64];
-  __shared__ __align__(16) uint32_t s_w[WK][kSlotDwords];
+  __shared__ float s_red[kWaves][2 * NI][64];
+  __shared__ __align__(16) uint32_t s_w[kWaves][kSlotDwords];
 
   const int n_tiles = p.size_n >> 6;
-  const int nt = blockIdx.x % n_tiles;
-  const int split = blockIdx.x / n_tiles;
+  const int n_units = kPair ? (p.inter >> 6) : n_tiles;  // column units per K share
+  const int split = blockIdx.x / n_units;
   const int mb = blockIdx.y;
   int ntp = p.ntp[0];
   if (ntp > p.sorted_len) ntp = p.sorted_len;
@@ -238,6 +243,9 @@ __global__ __launch_bounds__(64 * WK, 4) void wna16_decode_kernel(GemmArgs p) {
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kw = wave % WK;    // this wave's K share
+  const int half = wave / WK;  // with kPair: 0 gate tile, 1 up tile
+  const int nt = blockIdx.x % n_units + (kPair ? half * (p.inter >> 6) : 0);
   const int valid_limit = p.size_m * p.top_k;
   if (tid < 32) {
     int sid = valid_limit;
@@ -251,7 +259,7 @@ __global__ __launch_bounds__(64 * WK, 4) void wna16_decode_kernel(GemmArgs p) {
   const int groups = K >> 5;
   // this workgroup's share of the K groups, then this wave's share of that
   const int gs0 = (groups * split) / p.splits, gs1 = (groups * (split + 1)) / p.splits;
-  const int g0 = gs0 + ((gs1 - gs0) * wave) / WK, g1 = gs0 + ((gs1 - gs0) * (wave + 1)) / WK;
+  const int g0 = gs0 + ((gs1 - gs0) * kw) / WK, g1 = gs0 + ((gs1 - gs0) * (kw + 1)) / WK;
 
   const uint32_t expert_bytes = static_cast<uint32_t>(N) * static_cast<uint32_t>(K) / 2u;
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(
@@ -342,6 +350,27 @@ __global__ __launch_bounds__(64 * WK, 4) void wna16_decode_kernel(GemmArgs p) {
   }
   __syncthreads();
 
+  if constexpr (kPair) {
+    // the same (row, column) of the gate and the up tile: SwiGLU of the two sums
+    const int col0 = (blockIdx.x % n_units) * 64 + (c >> 3) * 16 + (c & 7);
+    for (int j = wave; j < 2 * NI; j += kWaves) {
+      float sg = 0.0f, su = 0.0f;
+#pragma unroll
+      for (int w = 0; w < WK; ++w) {
+        sg += s_red[w][j][lane];
+        su += s_red[WK + w][j][lane];
+      }
+      const int row = acc_row(j < NI ? j : j - NI, h);
+      const int col = (j < NI) ? col0 : col0 + 8;
+      if (row < p.bs) {
+        const int sid = s_sid[row];
+        if (static_cast<unsigned>(sid) < static_cast<unsigned>(valid_limit))
+          p.act[static_cast<long long>(sid) * p.inter + col] =
+              swiglu_one(bf2f(f2bf(sg)), bf2f(f2bf(su)));
+      }
+    }
+    return;
+  }
   const int n0 = nt * 64 + (c >> 3) * 16 + (c & 7);
   for (int j = wave; j < 2 * NI; j += WK) {
     float s = 0.0f;
@@ -372,6 +401,17 @@ void launch_decode(const GemmArgs& args, int max_m_blocks, hipStream_t stream) {
   else
     hipLaunchKernelGGL((wna16_decode_kernel<WK, 8, kDecodeDepth>), grid, dim3(64 * WK), 0, stream,
                        args);
+}
+
+template <int WK>
+void launch_decode_pair(const GemmArgs& args, int max_m_blocks, hipStream_t stream) {
+  const dim3 grid(args.inter / 64, max_m_blocks);
+  if (args.bs <= 8)
+    hipLaunchKernelGGL((wna16_decode_kernel<WK, 4, kDecodeDepth, true>), grid, dim3(128 * WK), 0,
+                       stream, args);
+  else
+    hipLaunchKernelGGL((wna16_decode_kernel<WK, 8, kDecodeDepth, true>), grid, dim3(128 * WK), 0,
+                       stream, args);
 }
 
 // ---------------------------------------------------------------------------
@@ -928,24 +968,35 @@ int wna16_w13_swiglu(const uint16_t* input, uint16_t* act, float* partials, long
                        dim3(256), 0, stream, args);
     return launch_status("w13_swiglu (prefill)");
   }
-  if (!partials) return fail(kInvalidValue, "w13_swiglu: partials required for block sizes 8, 16");
-  const long long routes = static_cast<long long>(size_m) * top_k;
-  if (partials_len < routes * size_n)
-    return fail(kInvalidValue, "w13_swiglu: partials holds %lld floats, needs >= %lld",
-                partials_len, routes * size_n);
   if (cu_count <= 0) cu_count = current_cu_count();
   if (cu_count <= 0) return fail(kInvalidValue, "w13_swiglu: no device");
-
+  const long long routes = static_cast<long long>(size_m) * top_k;
   const int n_tiles = size_n / 64;
   const int groups = size_k / 32;
   const long long est_blocks = routes < max_m_blocks ? routes : max_m_blocks;
   const long long wgs = est_blocks * n_tiles;
-  // shares: about two workgroups per CU, at least 8 groups (two per wave) each
+  // shares: about two workgroups per CU, at least 8 groups (two per wave) each,
+  // as many as the partials buffer holds
   long long sp = (2LL * cu_count + wgs - 1) / wgs;
   if (sp > 16) sp = 16;
   if (sp > groups / 8) sp = groups / 8;
-  if (sp > partials_len / (routes * size_n)) sp = partials_len / (routes * size_n);
-  const int splits = sp > 1 ? static_cast<int>(sp) : 1;
+  const long long cap = partials ? partials_len / (routes * size_n) : 0;
+  if (sp > cap) sp = cap;
+  if (sp <= 1) {
+    // No K split: a gate tile and its up tile in one workgroup of 2 WK waves,
+    // SwiGLU in the epilogue (partials not used).
+    GemmArgs args{input, nullptr, nullptr, reinterpret_cast<const uint32_t*>(b_qweight),
+                  b_scales, nullptr, sorted_token_ids, expert_ids, num_tokens_post_padded,
+                  nullptr, sorted_token_ids_len, moe_block_size, top_k, 0, size_m, size_n,
+                  size_k, local_experts, 1, nullptr, act, inter};
+    const long long pair_wgs = est_blocks * (inter / 64);
+    int wk = pair_wgs >= 2LL * cu_count ? 4 : 8;
+    while (wk > 4 && groups < 2 * wk) wk >>= 1;  // keep >= 2 groups per wave
+    if (wk == 4) launch_decode_pair<4>(args, max_m_blocks, stream);
+    else launch_decode_pair<8>(args, max_m_blocks, stream);
+    return launch_status("w13_swiglu (decode)");
+  }
+  const int splits = static_cast<int>(sp);
   GemmArgs args{input, nullptr, nullptr, reinterpret_cast<const uint32_t*>(b_qweight), b_scales,
                 nullptr, sorted_token_ids, expert_ids, num_tokens_post_padded, nullptr,
                 sorted_token_ids_len, moe_block_size, top_k, 0, size_m, size_n, size_k,

@@ -71,8 +71,8 @@ class RoutedExperts:
                 out_f32: torch.Tensor, combine: str = "sum", w13_timer=None,
                 reference_flow: bool = False) -> torch.Tensor:
         """Routed-expert forward (moe_nccl.rs:152-203 order: align, W13, SwiGLU, W2
-        with the top-k weight, top-k combine).  With prefill block sizes (> 16) W13
-        and SwiGLU are one call unless reference_flow is set.
+        with the top-k weight, top-k combine).  W13 and SwiGLU are one call unless
+        reference_flow is set.
 
         combine "sum": the weight is applied in the W2 epilogue and rows are summed
         (Kimi); "weighted": W2 without weight and an fmaf-chain combine (DSV2).
@@ -92,8 +92,9 @@ class RoutedExperts:
         if reference_flow:
             w13_out.zero_()
         mark = w13_timer.start() if w13_timer is not None else None
-        if not reference_flow and routing.block_size > 16:
-            # prefill: SwiGLU in the W13 tile epilogue, routed rows only (same bits)
+        if not reference_flow:
+            # SwiGLU in the W13 epilogue (gate and up tiles in one workgroup), routed rows
+            # only, same bits as W13 then SwiGLU
             ops.wna16_w13_swiglu(self.gemm_ws, routing, hidden, self.w13, act, top_k=self.topk,
                                  size_m=T)
             if w13_timer is not None:

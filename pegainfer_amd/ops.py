@@ -421,18 +421,20 @@ def wna16_gemm(workspace: KimiMarlinWna16Workspace, routing: KimiMarlinRouting,
 
 def wna16_w13_swiglu(workspace: KimiMarlinWna16Workspace, routing: KimiMarlinRouting,
                      input: torch.Tensor, weight: MarlinInt4Weight, act: torch.Tensor, *,
-                     top_k: int, size_m: int) -> None:
+                     top_k: int, size_m: int, split_k: bool = True) -> None:
     """act[sorted_id] = SwiGLU(bf16(A[sorted_id / top_k] . dequant(W13[expert]))) in one
-    call, routed rows only.  Block sizes 8/16: K split across workgroups, the partials (the
-    workspace's c_tmp) summed by the SwiGLU kernel; 32/48/64: the tile GEMM with a SwiGLU
-    epilogue."""
+    call, routed rows only.  Block sizes 8/16: when too few workgroups would fill the GPU,
+    K is split across workgroups and the partials (the workspace's c_tmp) are summed by the
+    SwiGLU kernel; otherwise (or with split_k=False) a gate tile and its up tile share a
+    workgroup with SwiGLU in the epilogue.  32/48/64: the tile GEMM with a SwiGLU epilogue."""
     inter = weight.out_dim // 2
     _ensure(workspace.block_size == routing.block_size, "workspace / routing block size differ")
     _ensure(2 * inter <= workspace.max_size_n, "W13 width exceeds the workspace")
     _ensure(act.dtype == torch.bfloat16 and act.numel() >= size_m * top_k * inter,
             "act must be bf16 [size_m * top_k, inter]")
-    _lib.call("pega_wna16_w13_swiglu", _ptr(input), _ptr(act), _ptr(workspace.c_tmp),
-              workspace.c_tmp.numel(), _ptr(weight.weight_packed_uint4b8),
+    _lib.call("pega_wna16_w13_swiglu", _ptr(input), _ptr(act),
+              _ptr(workspace.c_tmp) if split_k else None,
+              workspace.c_tmp.numel() if split_k else 0, _ptr(weight.weight_packed_uint4b8),
               _ptr(weight.weight_scale_permuted), _ptr(routing.sorted_token_ids),
               _ptr(routing.expert_ids), _ptr(routing.num_tokens_post_padded),
               routing.sorted_token_ids.numel(), routing.block_size, top_k, size_m, inter,

@@ -170,17 +170,21 @@ def test_gemm_block8_four_waves_exact(oracle):
     assert np.array_equal(got, ref)
 
 
-@pytest.mark.parametrize("E,T,topk,bs,inter,K", [(1, 1, 1, 8, 2048, 7168), (1, 8, 1, 8, 1024, 2048),
-                                                 (48, 4, 8, 16, 512, 1024),
-                                                 (3, 300, 4, 32, 192, 256),
-                                                 (48, 160, 8, 48, 1024, 512),
-                                                 (4, 512, 2, 64, 1408, 256)])
-def test_w13_swiglu_fused_exact(oracle, E, T, topk, bs, inter, K):
+@pytest.mark.parametrize("E,T,topk,bs,inter,K,split_k", [
+    (1, 1, 1, 8, 2048, 7168, True), (1, 8, 1, 8, 1024, 2048, True), (48, 4, 8, 16, 512, 1024, True),
+    (1, 1, 1, 8, 2048, 7168, False), (1, 8, 1, 8, 1024, 2048, False),
+    (48, 4, 8, 16, 512, 1024, False), (48, 64, 8, 16, 512, 1024, True),
+    (3, 300, 4, 32, 192, 256, True), (48, 160, 8, 48, 1024, 512, True),
+    (4, 512, 2, 64, 1408, 256, True)])
+def test_w13_swiglu_fused_exact(oracle, E, T, topk, bs, inter, K, split_k):
     """pega_wna16_w13_swiglu on exact inputs: every W13 value is exact, so the
     activations equal oracle SwiGLU(oracle W13) bit for bit; rows of routes that are
-    not local keep their contents.  Block sizes 8/16 take the split-K path (partials
-    summed and rounded by the SwiGLU kernel), 32/48/64 the tile GEMM with the SwiGLU
-    epilogue (an odd gate-tile count leaves a workgroup half its columns)."""
+    not local keep their contents.  Block sizes 8/16 split K across workgroups when the
+    units are few (partials summed and rounded by the SwiGLU kernel) and otherwise, or
+    with split_k=False, pair each gate tile with its up tile in one workgroup (SwiGLU in
+    the epilogue; the 48-expert, 64-token case picks that path by itself); 32/48/64 take
+    the tile GEMM with the SwiGLU epilogue (an odd gate-tile count leaves a workgroup half
+    its columns)."""
     from pegainfer_amd import ops
     g = np.random.default_rng(E * 100 + T)
     N = 2 * inter
@@ -195,7 +199,8 @@ def test_w13_swiglu_fused_exact(oracle, E, T, topk, bs, inter, K):
     gws = ops.KimiMarlinWna16Workspace(ws.max_m_blocks, N, bs, extra_splits=16)
     act = torch.full((T * topk, inter), 3.0, dtype=torch.bfloat16, device="cuda")
     for _ in range(2):
-        ops.wna16_w13_swiglu(gws, routing, dev(a_bits), w, act, top_k=topk, size_m=T)
+        ops.wna16_w13_swiglu(gws, routing, dev(a_bits), w, act, top_k=topk, size_m=T,
+                             split_k=split_k)
     got = host(act)
     r = {k: host(v) for k, v in (("sorted_token_ids", routing.sorted_token_ids),
                                  ("expert_ids", routing.expert_ids),

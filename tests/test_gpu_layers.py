@@ -41,8 +41,8 @@ def _routed_layer(gate, up, down, *, tokens, topk, block_size, global_start=0):
 
 def _unfused_w13(routed, hidden_dev, topk_w_dev, T):
     """The W13 GEMM alone (bf16 output) with the layer's routing, into a zeroed
-    buffer.  The prefill layer fuses SwiGLU into W13, so its activations must be
-    SwiGLU of exactly these bits."""
+    buffer.  The layer fuses SwiGLU into W13, so its activations must be SwiGLU of
+    exactly these bits."""
     from pegainfer_amd import ops
     out = torch.zeros(T * routed.topk, 2 * routed.I, dtype=torch.bfloat16, device="cuda")
     ops.wna16_gemm(routed.gemm_ws, routed.routing, hidden_dev, routed.w13, topk_w_dev, out,
@@ -118,8 +118,9 @@ def test_c3_kimi_decode_layer(oracle):
     out = torch.zeros(T, H, dtype=torch.float32, device="cuda")
     # a first call with other routes leaves stale rows behind: the default flow
     # skips the zero-fills, so only rows of local routes may be compared below
-    moe.forward(dev(hidden), ((idx + 11) % 384).contiguous(), w, out)
-    moe.forward(dev(hidden), idx, w, out)
+    hidden_d = dev(hidden)
+    moe.forward(hidden_d, ((idx + 11) % 384).contiguous(), w, out)
+    moe.forward(hidden_d, idx, w, out)
     local = (ref_idx.reshape(-1) < E)
 
     routing = _routing_host(moe.routing)
@@ -127,7 +128,7 @@ def test_c3_kimi_decode_layer(oracle):
     assert np.array_equal(routing["sorted_token_ids"], ref_r["sorted_token_ids"])
     w13p = np.concatenate([gate[0], up[0]], axis=1)
     w13s = np.concatenate([gate[1], up[1]], axis=1)
-    g13 = host(moe.w13_out[:T * 8])
+    g13 = _unfused_w13(moe, hidden_d, w, T)  # the layer fuses SwiGLU into W13
     ref13 = oracle.wna16_gemm(hidden, w13p, w13s, routing, ref_w, moe_block_size=bs, top_k=8,
                               mul_topk_weights=False, size_m=T, size_n=2 * I, size_k=H, threads=16)
     assert_bf16_close(g13[local], ref13[local], what="C3 W13")
@@ -141,7 +142,8 @@ def test_c3_kimi_decode_layer(oracle):
     ro[~local] = 0
     got = host(out)
     assert np.array_equal(got, oracle.sum_topk_rows(ro, T, 8, H))
-    # the reference's call sequence (zero-fills + full combine) gives the same bits
+    # the reference's call sequence (zero-fills, W13 then SwiGLU, full combine) gives the
+    # same bits
     out_ref_flow = torch.zeros_like(out)
     moe.forward(dev(hidden), idx, w, out_ref_flow, reference_flow=True)
     assert np.array_equal(host(out_ref_flow).view(np.uint32), got.view(np.uint32))

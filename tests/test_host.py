@@ -137,10 +137,13 @@ def test_fused_w13_swiglu_rejects_bad_arguments():
                      base["k"], base["experts"], base["group"], 0, NULL)
     assert call(bs=24)[0] == 1             # block sizes 8, 16, 32, 48, 64 only
     assert call(group=64)[0] == 1
-    assert call(partials=NULL)[0] == 1
-    rc, msg = call(partials_len=100)
-    assert rc == 1 and "partials" in msg  # fewer floats than one share needs
     assert call(inter=2000)[0] == 801      # width must be a multiple of 64
+    assert call(k=7160)[0] == 801          # K must be a multiple of 64
+    assert call(m=0)[0] == 1
+    odd = ctypes.c_void_p(0x1008)
+    rc = _call("pega_wna16_w13_swiglu", FAKE, odd, FAKE, ctypes.c_longlong(1 << 20), FAKE, FAKE,
+               FAKE, FAKE, FAKE, 15, 8, 1, 1, 2048, 7168, 1, 32, 0, NULL)[0]
+    assert rc == 1                         # act is written with 16-byte stores
 
 
 # ------------------------------------------------------------- Python mirror logic
