@@ -126,11 +126,13 @@ class DenseW4A16:
     static identity routing)."""
 
     def __init__(self, w: ops.MarlinInt4Weight, *, max_rows: int, device="cuda",
-                 extra_splits: int = 8):
+                 extra_splits: int = 8, block_size: int = None):
         assert w.local_experts == 1
         self.w = w
         self.max_rows = max_rows
-        self.block_size = 8 if max_rows <= 8 else (16 if max_rows <= 16 else 64)
+        if block_size is None:
+            block_size = 8 if max_rows <= 8 else (16 if max_rows <= 16 else 64)
+        self.block_size = block_size
         self.route_ws = ops.KimiMarlinRouteWorkspace(max_rows, self.block_size, device=device,
                                                      topk=1, local_experts=1)
         self.gemm_ws = ops.KimiMarlinWna16Workspace(self.route_ws.max_m_blocks, w.out_dim,
@@ -157,9 +159,11 @@ class ExpertFFN:
     """One expert: W13 -> SwiGLU -> W2 (no routing weight), bf16 out."""
 
     def __init__(self, w13: ops.MarlinInt4Weight, w2: ops.MarlinInt4Weight, *, max_rows: int,
-                 device="cuda", extra_splits: int = 8):
-        self.up = DenseW4A16(w13, max_rows=max_rows, device=device, extra_splits=extra_splits)
-        self.down = DenseW4A16(w2, max_rows=max_rows, device=device, extra_splits=extra_splits)
+                 device="cuda", extra_splits: int = 8, block_size: int = None):
+        self.up = DenseW4A16(w13, max_rows=max_rows, device=device, extra_splits=extra_splits,
+                             block_size=block_size)
+        self.down = DenseW4A16(w2, max_rows=max_rows, device=device, extra_splits=extra_splits,
+                               block_size=block_size)
         self.I = w13.out_dim // 2
         bf = dict(dtype=torch.bfloat16, device=device)
         self.h13 = torch.zeros(max_rows, w13.out_dim, **bf)
@@ -188,20 +192,35 @@ class Dsv2MoeLayer:
     in the fp32 combine, route order = expert id) plus a shared expert, joined
     as bf16(routed_f32 + shared) (kimi_add_f32_bf16_to_bf16 rounding)."""
 
-    def __init__(self, routed: RoutedExperts, shared: ExpertFFN, device="cuda"):
+    def __init__(self, routed: RoutedExperts, shared: ExpertFFN, device="cuda",
+                 overlap_shared: bool = True):
         self.routed, self.shared = routed, shared
         T, H = routed.max_tokens, routed.H
         self.topk_w = torch.zeros(T, routed.topk, dtype=torch.float32, device=device)
         self.topk_idx = torch.zeros(T, routed.topk, dtype=torch.int32, device=device)
         self.routed_f32 = torch.zeros(T, H, dtype=torch.float32, device=device)
         self.shared_out = torch.zeros(T, H, dtype=torch.bfloat16, device=device)
+        # the shared expert's stream (default priority, like every stream here)
+        self.side = torch.cuda.Stream(device=device) if overlap_shared else None
 
     def forward(self, hidden: torch.Tensor, logits: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+        """The shared expert does not depend on the routed branch, so by default it
+        runs on a second stream: its few large workgroups (one expert, 512 rows)
+        share the GPU with the routed kernels instead of running after them.  The
+        streams join before the add; the kernels and their bits are the same."""
         T = hidden.shape[0]
+        main = torch.cuda.current_stream()
+        if self.side is not None:
+            self.side.wait_stream(main)
+            with torch.cuda.stream(self.side):
+                self.shared.forward(hidden, self.shared_out[:T])
         ops.dsv2_router_select(logits, self.topk_w[:T], self.topk_idx[:T], T, self.routed.topk)
         self.routed.forward(hidden, self.topk_idx[:T], self.topk_w[:T], self.routed_f32[:T],
                             combine="weighted")
-        self.shared.forward(hidden, self.shared_out[:T])
+        if self.side is not None:
+            main.wait_stream(self.side)
+        else:
+            self.shared.forward(hidden, self.shared_out[:T])
         ops.kimi_add_f32_bf16_to_bf16(self.routed_f32[:T], self.shared_out[:T], out)
         return out
 
