@@ -10,14 +10,16 @@
 // the sentinel route_elems; expert_ids[b] = e for every block of the segment
 // and -1 past the total.  The reference meets this order only on its
 // single-block path (< 1024 routes); its 4-launch path takes positions from an
-// atomic cursor, so the order inside an expert varies run to run.  This
-// implementation is one deterministic launch of one workgroup for every size:
-// each of the 16 waves owns a contiguous run of 64-route steps; inside a step
-// the lanes holding the same expert find each other with one ballot per bit
-// of the expert id, so a lane's rank among them is a popcount.  Per-(wave,
-// expert) counts in LDS are scanned down the wave axis and across experts,
-// and the scatter replays every step in order -- a stable counting sort,
-// bit-exact with the contract.
+// atomic cursor, so the order inside an expert varies run to run.  Both paths
+// here are deterministic at every size.  Below 4096 routes it is one launch
+// of one workgroup: each of the 16 waves owns a contiguous run of 64-route
+// steps; inside a step the lanes holding the same expert find each other with
+// one ballot per bit of the expert id, so a lane's rank among them is a
+// popcount.  Per-(wave, expert) counts in LDS are scanned down the wave axis
+// and across experts, and the scatter replays every step in order -- a
+// stable counting sort, bit-exact with the contract.  From 4096 routes a
+// count launch and a scatter launch with one workgroup per expert produce the
+// same bytes (the wide path below).
 #include "common.h"
 
 namespace pega {
@@ -215,6 +217,142 @@ bool valid_block_size(int bs) { return bs == 8 || (bs >= 16 && bs <= 64 && bs % 
 
 }  // namespace
 
+// Wide path for large route counts: one workgroup per local expert, each
+// scanning every route for its own expert id, so each route costs one compare
+// and one ballot per expert instead of a ballot per id bit, and the work
+// spreads over E compute units.  The route ids stay in L2 (4 B a route).
+// Launch 1 counts each expert's routes into expert_cursor (its final value);
+// launch 2 turns the counts into padded segment starts and writes each
+// expert's segment in ascending route order: the same stable contract as the
+// single-workgroup kernel, so both produce the same bytes.
+
+// Routes in 64-route steps [s0, s1) whose id is `key` (wave-uniform result).
+__device__ __forceinline__ int wave_count_key(const int32_t* __restrict__ topk_idx, int route_elems,
+                                              int key, int s0, int s1) {
+  const int lane = threadIdx.x & 63;
+  int n = 0;
+  for (int s = s0; s < s1; s += kAlignBatch) {
+    int v[kAlignBatch];
+#pragma unroll
+    for (int j = 0; j < kAlignBatch; ++j) {
+      const int r = (s + j) * 64 + lane;
+      v[j] = (s + j < s1 && r < route_elems) ? topk_idx[r] : -1;
+    }
+#pragma unroll
+    for (int j = 0; j < kAlignBatch; ++j) n += __popcll(__ballot(v[j] == key));
+  }
+  return n;
+}
+
+// This wave's share of the 64-route steps: waves own contiguous runs so that
+// a wave's matches follow every match of the waves before it.
+__device__ __forceinline__ void wave_steps(int route_elems, int& s0, int& s1) {
+  const int steps = ceil_div(route_elems, 64);
+  const int per_wave = ceil_div(steps, kAlignWaves);
+  s0 = min((threadIdx.x >> 6) * per_wave, steps);
+  s1 = min(s0 + per_wave, steps);
+}
+
+__global__ __launch_bounds__(kAlignThreads) void align_count_kernel(
+    const int32_t* __restrict__ topk_idx, uint32_t* __restrict__ expert_cursor, int route_elems,
+    int global_start) {
+  __shared__ int s_n[kAlignWaves];
+  int s0, s1;
+  wave_steps(route_elems, s0, s1);
+  const int n = wave_count_key(topk_idx, route_elems, global_start + static_cast<int>(blockIdx.x),
+                               s0, s1);
+  if ((threadIdx.x & 63) == 0) s_n[threadIdx.x >> 6] = n;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int total = 0;
+    for (int w = 0; w < kAlignWaves; ++w) total += s_n[w];
+    expert_cursor[blockIdx.x] = static_cast<uint32_t>(total);
+  }
+}
+
+__global__ __launch_bounds__(kAlignThreads) void align_scatter_kernel(
+    const int32_t* __restrict__ topk_idx, int32_t* __restrict__ sorted_token_ids,
+    int32_t* __restrict__ expert_ids, int32_t* __restrict__ num_tokens_post_padded,
+    uint32_t* __restrict__ expert_offsets, const uint32_t* __restrict__ expert_cursor,
+    int route_elems, int global_start, int local_experts, int block_size, int max_padded_tokens,
+    int max_m_blocks) {
+  __shared__ int s_before[kAlignWaves], s_total[kAlignWaves], s_n[kAlignWaves];
+  const int e = blockIdx.x, t = threadIdx.x, wave = t >> 6, lane = t & 63;
+  const int key = global_start + e;
+  // the counts' loads go out with the recount's
+  const int count_t = t < local_experts ? static_cast<int>(expert_cursor[t]) : 0;
+  const int count = static_cast<int>(expert_cursor[e]);
+  int s0, s1;
+  wave_steps(route_elems, s0, s1);
+  const int n = wave_count_key(topk_idx, route_elems, key, s0, s1);
+
+  // padded segment sizes of all experts (thread t holds expert t): this
+  // segment's start is the sum over experts below e, the total over all
+  const int padded = ceil_div(count_t, block_size) * block_size;
+  int below_e = t < e ? padded : 0, all = padded;
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) {
+    below_e += __shfl_xor(below_e, d, 64);
+    all += __shfl_xor(all, d, 64);
+  }
+  if (lane == 0) {
+    s_before[wave] = below_e;
+    s_total[wave] = all;
+    s_n[wave] = n;
+  }
+  __syncthreads();
+  int start = 0, total = 0, rank = 0;
+  for (int w = 0; w < kAlignWaves; ++w) {
+    start += s_before[w];
+    total += s_total[w];
+    rank += w < wave ? s_n[w] : 0;
+  }
+  const int seg_end = start + ceil_div(count, block_size) * block_size;
+
+  // this wave's matches in ascending route order, after the earlier waves'
+  const uint64_t below = (1ull << lane) - 1ull;
+  for (int s = s0; s < s1; s += kAlignBatch) {
+    int v[kAlignBatch];
+#pragma unroll
+    for (int j = 0; j < kAlignBatch; ++j) {
+      const int r = (s + j) * 64 + lane;
+      v[j] = (s + j < s1 && r < route_elems) ? topk_idx[r] : -1;
+    }
+#pragma unroll
+    for (int j = 0; j < kAlignBatch; ++j) {
+      const bool hit = v[j] == key;
+      const uint64_t m = __ballot(hit);
+      const int pos = start + rank + __popcll(m & below);
+      if (hit && pos < max_padded_tokens) sorted_token_ids[pos] = (s + j) * 64 + lane;
+      rank += __popcll(m);
+    }
+  }
+
+  // the segment's padding and block ids; the tail past the total is shared
+  // out over the whole grid
+  for (int q = start + count + t; q < seg_end && q < max_padded_tokens; q += kAlignThreads)
+    sorted_token_ids[q] = route_elems;
+  for (int b = start / block_size + t; b < seg_end / block_size && b < max_m_blocks;
+       b += kAlignThreads)
+    expert_ids[b] = e;
+  const int g = e * kAlignThreads + t, gstride = gridDim.x * kAlignThreads;
+  for (int q = total + g; q < max_padded_tokens; q += gstride) sorted_token_ids[q] = route_elems;
+  for (int b = total / block_size + g; b < max_m_blocks; b += gstride) expert_ids[b] = -1;
+  if (t == 0) {
+    expert_offsets[e] = static_cast<uint32_t>(start);
+    if (e == 0) {
+      expert_offsets[local_experts] = static_cast<uint32_t>(total);
+      num_tokens_post_padded[0] = total;
+    }
+  }
+}
+
+// Route counts from which the per-expert path replaces the single workgroup
+// (below it the one launch is shorter than two).
+#ifndef PEGA_ALIGN_WIDE_MIN_ROUTES
+#define PEGA_ALIGN_WIDE_MIN_ROUTES 4096
+#endif
+
 // Shape-general permutation (local_experts <= 512, any topk); the Kimi
 // entry point below adds the reference's fixed-shape guards.
 int align_block_size(const int32_t* topk_idx, int32_t* sorted_token_ids, int32_t* expert_ids,
@@ -242,6 +380,15 @@ int align_block_size(const int32_t* topk_idx, int32_t* sorted_token_ids, int32_t
     return fail(kInvalidValue,
                 "align_block_size: capacity too small (padded %d < %lld or blocks %d < %d)",
                 max_padded_tokens, req_padded, max_m_blocks, required_blocks);
+  if (route_elems >= PEGA_ALIGN_WIDE_MIN_ROUTES) {
+    hipLaunchKernelGGL(align_count_kernel, dim3(local_experts), dim3(kAlignThreads), 0, stream,
+                       topk_idx, expert_cursor, route_elems, global_start);
+    hipLaunchKernelGGL(align_scatter_kernel, dim3(local_experts), dim3(kAlignThreads), 0, stream,
+                       topk_idx, sorted_token_ids, expert_ids, num_tokens_post_padded,
+                       expert_offsets, expert_cursor, route_elems, global_start, local_experts,
+                       block_size, max_padded_tokens, max_m_blocks);
+    return launch_status("align_block_size");
+  }
   const size_t lds = sizeof(uint32_t) * kAlignWaves * local_experts +
                      sizeof(int) * (local_experts + 1 + kAlignWaves);
   hipLaunchKernelGGL(align_block_size_kernel, dim3(1), dim3(kAlignThreads), lds, stream, topk_idx,

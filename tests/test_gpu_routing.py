@@ -78,7 +78,28 @@ def test_align_edge_cases(oracle):
     _check_against_oracle(oracle, ws, idx, 0, 48, 16)
 
 
+@pytest.mark.parametrize("tokens", [511, 512, 513, 5000])
+def test_align_wide_path_edges(oracle, tokens):
+    """From 4096 routes the permutation runs one workgroup per expert; these
+    straddle that switch (511/512/513 tokens x top-8) and repeat the edge
+    cases at a size on the wide path."""
+    g = np.random.default_rng(tokens)
+    idx = g.integers(0, 384, size=(tokens, 8)).astype(np.int32)
+    ws, _ = _gpu_align(idx, tokens, 8, 100, 48, 32)
+    _check_against_oracle(oracle, ws, idx, 100, 48, 32)
+    for fill, bs in ((300, 16), (17, 64)):  # no local route; every route to one expert
+        idx = np.full((tokens, 8), fill, np.int32)
+        ws, _ = _gpu_align(idx, tokens, 8, 0, 48, bs)
+        _check_against_oracle(oracle, ws, idx, 0, 48, bs)
+    # every expert present, routes in descending expert order
+    idx = (47 - np.arange(tokens * 8, dtype=np.int32) % 48).reshape(tokens, 8)
+    ws, _ = _gpu_align(idx, tokens, 8, 0, 48, 8)
+    _check_against_oracle(oracle, ws, idx, 0, 48, 8)
+
+
 @pytest.mark.parametrize("E,topk,tokens,bs", [(64, 6, 512, 64), (1, 1, 8, 8), (1, 1, 513, 64),
+                                              (1, 1, 9000, 64), (512, 4, 2048, 8),
+                                              (8, 8, 70000, 64),
                                               (224, 8, 100, 16), (512, 8, 3000, 32),
                                               (37, 3, 70000, 48)])
 def test_align_general_shapes(oracle, E, topk, tokens, bs):
