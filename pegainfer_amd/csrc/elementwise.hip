@@ -128,43 +128,94 @@ __global__ void weighted_topk_sum_kernel(const uint16_t* __restrict__ route,
 // k ascending from +0.  A skipped row would have added +0 (or fma(0, w, acc)
 // with finite w), which never changes a sum that starts at +0, so the result
 // equals the zero-filled full combine bit for bit.
-template <bool kWeighted>
-__global__ void combine_local_vec_kernel(const uint16_t* __restrict__ route,
-                                         const int32_t* __restrict__ topk_idx,
-                                         const float* __restrict__ weights,
-                                         float* __restrict__ out, int tokens, int topk,
-                                         int hidden, int global_start, int local_experts) {
-  const int per_row = hidden >> 3;
-  const long long total = static_cast<long long>(tokens) * per_row;
-  for (long long idx = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
-       idx += static_cast<long long>(gridDim.x) * blockDim.x) {
-    const long long t = idx / per_row;
-    const int d8 = static_cast<int>(idx - t * per_row) * 8;
-    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int k = 0; k < topk; ++k) {
-      const unsigned e = static_cast<unsigned>(topk_idx[t * topk + k] - global_start);
-      if (e >= static_cast<unsigned>(local_experts)) continue;
-      const uint4 v = *reinterpret_cast<const uint4*>(route + (t * topk + k) * hidden + d8);
-      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-      if (kWeighted) {
-        const float wk = weights[t * topk + k];
+//
+// One workgroup per (token, 1024-column chunk): the token's expert ids and
+// weights are uniform over the workgroup (scalar loads), every local row's
+// 16-byte load is in flight before the first add, and each wave writes 2 KB
+// of the fp32 row.  kTopk > 0 fixes top-k at compile time (6 and 8 here).
+constexpr int kCombineThreads = 128;
+constexpr int kCombineCols = kCombineThreads * 8;
+
+template <bool kWeighted, int kTopk>
+__global__ __launch_bounds__(kCombineThreads) void combine_local_rows_kernel(
+    const uint16_t* __restrict__ route, const int32_t* __restrict__ topk_idx,
+    const float* __restrict__ weights, float* __restrict__ out, int topk_rt, int hidden,
+    int chunks, int global_start, int local_experts) {
+  constexpr int kMaxK = kTopk > 0 ? kTopk : 1;
+  const int topk = kTopk > 0 ? kTopk : topk_rt;
+  const long long t = blockIdx.x / chunks;
+  const int d8 = (static_cast<int>(blockIdx.x - t * chunks) * kCombineThreads + threadIdx.x) * 8;
+  if (d8 >= hidden) return;
+  const int32_t* idx = topk_idx + t * topk;
+  const uint16_t* rows = route + t * topk * hidden + d8;
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  auto add = [&](const uint4& v, float wk) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    if (kWeighted) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          acc[2 * i] = __builtin_fmaf(bf_lo(w[i]), wk, acc[2 * i]);
-          acc[2 * i + 1] = __builtin_fmaf(bf_hi(w[i]), wk, acc[2 * i + 1]);
-        }
-      } else {
+      for (int i = 0; i < 4; ++i) {
+        acc[2 * i] = __builtin_fmaf(bf_lo(w[i]), wk, acc[2 * i]);
+        acc[2 * i + 1] = __builtin_fmaf(bf_hi(w[i]), wk, acc[2 * i + 1]);
+      }
+    } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          acc[2 * i] += bf_lo(w[i]);
-          acc[2 * i + 1] += bf_hi(w[i]);
-        }
+      for (int i = 0; i < 4; ++i) {
+        acc[2 * i] += bf_lo(w[i]);
+        acc[2 * i + 1] += bf_hi(w[i]);
       }
     }
-    float4* o = reinterpret_cast<float4*>(out + t * hidden + d8);
-    o[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
-    o[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+  };
+  if (kTopk > 0) {
+    // ids (and weights) first, so that they arrive in one scalar load
+    int id[kMaxK];
+    float wt[kMaxK];
+#pragma unroll
+    for (int k = 0; k < kMaxK; ++k) {
+      id[k] = idx[k];
+      wt[k] = kWeighted ? weights[t * topk + k] : 0.0f;
+    }
+    bool local[kMaxK];
+    uint4 v[kMaxK];
+#pragma unroll
+    for (int k = 0; k < kMaxK; ++k) {
+      local[k] = static_cast<unsigned>(id[k] - global_start) < static_cast<unsigned>(local_experts);
+      v[k] = local[k] ? *reinterpret_cast<const uint4*>(rows + static_cast<long long>(k) * hidden)
+                      : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int k = 0; k < kMaxK; ++k)
+      if (local[k]) add(v[k], wt[k]);
+  } else {
+    for (int k = 0; k < topk; ++k) {
+      if (static_cast<unsigned>(idx[k] - global_start) >= static_cast<unsigned>(local_experts))
+        continue;
+      add(*reinterpret_cast<const uint4*>(rows + static_cast<long long>(k) * hidden),
+          kWeighted ? weights[t * topk + k] : 0.0f);
+    }
   }
+  float4* o = reinterpret_cast<float4*>(out + t * hidden + d8);
+  o[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+  o[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+}
+
+template <bool kWeighted>
+void launch_combine_local(const uint16_t* route, const int32_t* topk_idx, const float* weights,
+                          float* out, int tokens, int topk, int hidden, int global_start,
+                          int local_experts, hipStream_t stream) {
+  const int chunks = ceil_div(hidden, kCombineCols);
+  const dim3 grid(static_cast<unsigned>(static_cast<long long>(tokens) * chunks));
+  if (topk == 8)
+    hipLaunchKernelGGL((combine_local_rows_kernel<kWeighted, 8>), grid, dim3(kCombineThreads), 0,
+                       stream, route, topk_idx, weights, out, topk, hidden, chunks, global_start,
+                       local_experts);
+  else if (topk == 6)
+    hipLaunchKernelGGL((combine_local_rows_kernel<kWeighted, 6>), grid, dim3(kCombineThreads), 0,
+                       stream, route, topk_idx, weights, out, topk, hidden, chunks, global_start,
+                       local_experts);
+  else
+    hipLaunchKernelGGL((combine_local_rows_kernel<kWeighted, 0>), grid, dim3(kCombineThreads), 0,
+                       stream, route, topk_idx, weights, out, topk, hidden, chunks, global_start,
+                       local_experts);
 }
 
 // out = bf16( routed*scale + f(bf16(f(hidden) + f(projected))) )
@@ -292,15 +343,14 @@ PEGA_API int pega_moe_combine_local_f32(const uint16_t* route_output, const int3
   if (hidden_dim % 8 != 0 || !aligned16(route_output) || !aligned16(out))
     return fail(kInvalidValue, "combine_local: hidden_dim %% 8 and 16-byte alignment required");
   if (active_tokens == 0) return kSuccess;
-  const unsigned grid = grid_cap(static_cast<long long>(active_tokens) * (hidden_dim / 8), 1 << 20);
+  if (static_cast<long long>(active_tokens) * ceil_div(hidden_dim, kCombineCols) > 0x7fffffffLL)
+    return fail(kInvalidValue, "combine_local: tokens x column chunks overflows the grid");
   if (topk_weight)
-    hipLaunchKernelGGL(combine_local_vec_kernel<true>, dim3(grid), dim3(kThreads), 0, stream,
-                       route_output, topk_idx, topk_weight, out, active_tokens, topk, hidden_dim,
-                       global_start, local_experts);
+    launch_combine_local<true>(route_output, topk_idx, topk_weight, out, active_tokens, topk,
+                               hidden_dim, global_start, local_experts, stream);
   else
-    hipLaunchKernelGGL(combine_local_vec_kernel<false>, dim3(grid), dim3(kThreads), 0, stream,
-                       route_output, topk_idx, topk_weight, out, active_tokens, topk, hidden_dim,
-                       global_start, local_experts);
+    launch_combine_local<false>(route_output, topk_idx, topk_weight, out, active_tokens, topk,
+                                hidden_dim, global_start, local_experts, stream);
   return launch_status("combine_local");
 }
 

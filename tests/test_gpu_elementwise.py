@@ -69,10 +69,14 @@ def test_weighted_topk_sum_bit_exact(oracle):
 @pytest.mark.parametrize("T,topk,H,gs,E,weighted", [(64, 8, 7168, 0, 48, False),
                                                      (5, 8, 7168, 96, 48, False),
                                                      (512, 6, 2048, 0, 64, True),
-                                                     (33, 6, 2048, 16, 20, True)])
+                                                     (33, 6, 2048, 16, 20, True),
+                                                     (40, 5, 7168, 8, 30, True),
+                                                     (7, 3, 1032, 0, 10, False)])
 def test_combine_local_equals_zero_filled_combine(oracle, T, topk, H, gs, E, weighted):
     """pega_moe_combine_local_f32 never reads rows of non-local routes (they hold
-    NaN here) and equals the zero-filled full combine bit for bit."""
+    NaN here) and equals the zero-filled full combine bit for bit.  Top-k 8 and 6
+    take the compile-time paths, 5 and 3 the runtime one; 1032 columns end in a
+    partial 1024-column chunk."""
     from pegainfer_amd import ops
     g = np.random.default_rng(T + topk + gs)
     idx = g.integers(0, 384 if E == 48 else 64, size=(T, topk)).astype(np.int32)

@@ -124,6 +124,9 @@ def test_repack_and_elementwise_reject_bad_arguments():
                  NULL)[0] == 1
     assert _call("pega_moe_combine_local_f32", FAKE, FAKE, NULL, FAKE, 4, 8, 7168, 0, 0,
                  NULL)[0] == 1
+    # one workgroup per (token, 1024-column chunk): the grid must fit 2^31 - 1
+    assert _call("pega_moe_combine_local_f32", FAKE, FAKE, NULL, FAKE, 400_000_000, 8, 7168, 0,
+                 48, NULL)[0] == 1
 
 
 def test_fused_w13_swiglu_rejects_bad_arguments():
