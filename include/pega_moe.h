@@ -146,6 +146,39 @@ int pega_wna16_w13_swiglu(const uint16_t* input, uint16_t* act, float* partials,
                           int intermediate_dim, int size_k, int local_experts, int group_size,
                           int sm_count, hipStream_t stream);
 
+/* One problem of pega_wna16_prefill_pair: a grouped INT4 GEMM at a prefill block size (the
+ * 128-row tile kernel), as pega_wna16_gemm (act NULL) or pega_wna16_w13_swiglu (act set)
+ * would run it.  Plain pointers and sizes; 112 bytes on LP64. */
+typedef struct pega_wna16_problem {
+    const uint16_t* input;                /* bf16 [size_m, size_k], 16-byte aligned */
+    uint16_t* output;                     /* bf16 [size_m * top_k, size_n] (unused with act) */
+    uint16_t* act;                        /* non-NULL: SwiGLU epilogue into bf16
+                                             [size_m * top_k, size_n / 2] */
+    const uint8_t* b_qweight;             /* device-layout INT4 weights [local_experts] */
+    const uint16_t* b_scales;             /* device-layout bf16 scales */
+    const int32_t* sorted_token_ids;      /* the permutation of this problem's routes */
+    const int32_t* expert_ids;
+    const int32_t* num_tokens_post_padded;
+    const float* topk_weights;            /* read only with mul_topk_weights */
+    int sorted_token_ids_len;
+    int moe_block_size;                   /* 32, 48 or 64 */
+    int top_k;
+    int mul_topk_weights;                 /* 0 or 1 (0 with act) */
+    int size_m;
+    int size_n;                           /* with act: 2 * intermediate_dim, gate then up */
+    int size_k;
+    int local_experts;
+    int group_size;                       /* 32 */
+} pega_wna16_problem;
+
+/* No reference counterpart: two independent prefill-size GEMMs in one launch, e.g. a layer's
+ * shared expert (first) and its routed experts (second).  The workgroups of the first problem
+ * are dispatched first, and the second problem's fill the rest of the GPU, so one stream keeps
+ * both running at once; each problem's output has the bits its own single launch gives.
+ * Returns 801 when a problem's block size is 8 or 16 (the decode kernels). */
+int pega_wna16_prefill_pair(const pega_wna16_problem* first, const pega_wna16_problem* second,
+                            hipStream_t stream);
+
 /* ---------------- activation / combine / residual ---------------- */
 
 /* Replaces kimi_marlin_w13_swiglu_cuda, pegainfer-kernels/src/ffi/kimi.rs:113-119. */

@@ -18,6 +18,18 @@ _LL = ctypes.c_longlong
 _F = ctypes.c_float
 _B = ctypes.c_bool
 
+
+
+class Wna16Problem(ctypes.Structure):
+    """pega_wna16_problem (include/pega_moe.h): one problem of pega_wna16_prefill_pair."""
+    _fields_ = [("input", _P), ("output", _P), ("act", _P), ("b_qweight", _P),
+                ("b_scales", _P), ("sorted_token_ids", _P), ("expert_ids", _P),
+                ("num_tokens_post_padded", _P), ("topk_weights", _P),
+                ("sorted_token_ids_len", _I), ("moe_block_size", _I), ("top_k", _I),
+                ("mul_topk_weights", _I), ("size_m", _I), ("size_n", _I), ("size_k", _I),
+                ("local_experts", _I), ("group_size", _I)]
+
+
 # name -> argument types (return type is int unless listed in _RESTYPE)
 SIGNATURES = {
     "pegainfer_kernels_last_error": [],
@@ -44,6 +56,7 @@ SIGNATURES = {
     "kimi_add_f32_bf16_to_bf16_cuda": [_P, _P, _P, _I, _P],
     "pega_kimi_router_select": [_P, _P, _P, _P, _I, _I, _I, _F, _P],
     "pega_dsv2_router_select": [_P, _P, _P, _I, _I, _I, _P],
+    "pega_wna16_prefill_pair": [ctypes.POINTER(Wna16Problem), ctypes.POINTER(Wna16Problem), _P],
 }
 _RESTYPE = {"pegainfer_kernels_last_error": ctypes.c_char_p}
 

@@ -27,6 +27,7 @@
 // one 32-byte read.  Scales of n0 and n1 are adjacent in the permuted scale
 // row: index 8*(c%8) + 2*(c/8) (+1).
 #include "common.h"
+#include "pega_moe.h"
 
 namespace pega {
 namespace {
@@ -450,7 +451,7 @@ typedef uint16_t PfStage[kPfRows * kPfLdsStride];
 template <int RB>
 __device__ __forceinline__ void prefill_tile(const GemmArgs& p, PfStage* s_a, uint32_t* s_w_wave,
                                              const int* s_sid, const float* s_tw, int expert,
-                                             int nt) {
+                                             int nt, int tx) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int c = lane & 31, h = lane >> 5;
   const int K = p.size_k, N = p.size_n;
@@ -596,7 +597,7 @@ __device__ __forceinline__ void prefill_tile(const GemmArgs& p, PfStage* s_a, ui
     uint16_t* x16 = reinterpret_cast<uint16_t*>(s_a);
     const uint32_t* x32 = reinterpret_cast<const uint32_t*>(s_a);
     const int wave = threadIdx.x >> 6;
-    const int g0 = blockIdx.x * 2;  // first gate tile of this workgroup
+    const int g0 = tx * 2;  // first gate tile of this workgroup
     const int gate_tiles = p.inter >> 6;
 #pragma unroll
     for (int ph = 0; ph < 2; ++ph) {
@@ -678,7 +679,7 @@ __device__ __forceinline__ void prefill_tile(const GemmArgs& p, PfStage* s_a, ui
     __syncthreads();
     const int r = threadIdx.x >> 2, t4 = threadIdx.x & 3;
     const int sid = s_sid[64 * ph + r];
-    const int nt_t = blockIdx.x * 4 + t4;
+    const int nt_t = tx * 4 + t4;
     if (nt_t < (N >> 6) && static_cast<unsigned>(sid) < static_cast<unsigned>(valid_limit)) {
       const uint4* src = reinterpret_cast<const uint4*>(xo + r * kOStride + t4 * 64);
       uint4* dst = reinterpret_cast<uint4*>(p.output + static_cast<long long>(sid) * N + nt_t * 64);
@@ -698,7 +699,9 @@ __device__ __forceinline__ void prefill_tile(const GemmArgs& p, PfStage* s_a, ui
 // over shader engines then puts all the work on half of them.)
 constexpr int kPfScanSlab = 1024;  // block experts staged in LDS per scan pass
 
-__global__ __launch_bounds__(256, 2) void wna16_prefill_kernel(GemmArgs p) {
+// One workgroup's tile of a problem: column group tx, tile ty (the ty-th
+// 128-row tile start among the routed blocks).
+__device__ __forceinline__ void prefill_block(const GemmArgs& p, int tx, int ty) {
   __shared__ __align__(16) PfStage s_a[2];
   __shared__ __align__(16) uint32_t s_w[4][kSlotDwords];
   __shared__ int s_sid[kPfRows];
@@ -708,7 +711,6 @@ __global__ __launch_bounds__(256, 2) void wna16_prefill_kernel(GemmArgs p) {
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int ty = blockIdx.y;
   int ntp = p.ntp[0];
   if (ntp > p.sorted_len) ntp = p.sorted_len;
   const int nblocks = ntp / p.bs;
@@ -784,22 +786,39 @@ __global__ __launch_bounds__(256, 2) void wna16_prefill_kernel(GemmArgs p) {
   int nt;
   bool tile_ok;
   if (p.act != nullptr) {
-    const int gate = blockIdx.x * 2 + (wave & 1);
+    const int gate = tx * 2 + (wave & 1);
     tile_ok = gate < (p.inter >> 6);
     nt = wave < 2 ? gate : gate + (p.inter >> 6);
   } else {
-    nt = blockIdx.x * 4 + wave;
+    nt = tx * 4 + wave;
     tile_ok = nt < (p.size_n >> 6);
   }
   const int rb = tile_ok ? __builtin_amdgcn_readfirstlane((row_end + 31) >> 5) : 0;
   uint32_t* s_w_wave = s_w[wave];
   switch (rb) {
-    case 0: prefill_tile<0>(p, s_a, s_w_wave, s_sid, s_tw, expert, nt); break;
-    case 1: prefill_tile<1>(p, s_a, s_w_wave, s_sid, s_tw, expert, nt); break;
-    case 2: prefill_tile<2>(p, s_a, s_w_wave, s_sid, s_tw, expert, nt); break;
-    case 3: prefill_tile<3>(p, s_a, s_w_wave, s_sid, s_tw, expert, nt); break;
-    default: prefill_tile<4>(p, s_a, s_w_wave, s_sid, s_tw, expert, nt); break;
+    case 0: prefill_tile<0>(p, s_a, s_w_wave, s_sid, s_tw, expert, nt, tx); break;
+    case 1: prefill_tile<1>(p, s_a, s_w_wave, s_sid, s_tw, expert, nt, tx); break;
+    case 2: prefill_tile<2>(p, s_a, s_w_wave, s_sid, s_tw, expert, nt, tx); break;
+    case 3: prefill_tile<3>(p, s_a, s_w_wave, s_sid, s_tw, expert, nt, tx); break;
+    default: prefill_tile<4>(p, s_a, s_w_wave, s_sid, s_tw, expert, nt, tx); break;
   }
+}
+
+__global__ __launch_bounds__(256, 2) void wna16_prefill_kernel(GemmArgs p) {
+  prefill_block(p, blockIdx.x, blockIdx.y);
+}
+
+// Two independent problems in one launch (e.g. a layer's routed experts and
+// its shared expert): the flat grid holds the first problem's x0-by-y
+// workgroups, then the second's, each in its own x-fastest order, so one
+// stream keeps both on the GPU at once.
+__global__ __launch_bounds__(256, 2) void wna16_prefill_pair_kernel(GemmArgs p0, GemmArgs p1,
+                                                                    int x0, int n0, int x1) {
+  const int l = static_cast<int>(blockIdx.x);
+  if (l < n0)
+    prefill_block(p0, l % x0, l / x0);
+  else
+    prefill_block(p1, (l - n0) % x1, (l - n0) / x1);
 }
 
 // W13 finish fused with SwiGLU: for every routed row, the gate and up
@@ -1017,6 +1036,70 @@ int wna16_w13_swiglu(const uint16_t* input, uint16_t* act, float* partials, long
   return launch_status("w13_swiglu (SwiGLU)");
 }
 
+namespace {
+
+// Checks one problem of the pair entry and fills its kernel arguments and its
+// (column groups, m-blocks) grid.
+int prefill_problem(const pega_wna16_problem* q, const char* which, GemmArgs& args, int& gx,
+                    int& gy) {
+  if (!q) return fail(kInvalidValue, "wna16_prefill_pair: %s problem is NULL", which);
+  const bool swiglu = q->act != nullptr;
+  if (!q->input || (!swiglu && !q->output) || !q->b_qweight || !q->b_scales ||
+      !q->sorted_token_ids || !q->expert_ids || !q->num_tokens_post_padded ||
+      (q->mul_topk_weights && !q->topk_weights))
+    return fail(kInvalidValue, "wna16_prefill_pair: %s problem has a null pointer", which);
+  if (q->group_size != 32 || q->top_k <= 0 || q->size_m <= 0 || q->size_n <= 0 ||
+      q->size_k <= 0 || q->sorted_token_ids_len <= 0 || q->local_experts <= 0 ||
+      (q->mul_topk_weights != 0 && q->mul_topk_weights != 1))
+    return fail(kInvalidValue, "wna16_prefill_pair: %s problem has a bad shape m=%d n=%d k=%d",
+                which, q->size_m, q->size_n, q->size_k);
+  if (q->moe_block_size != 32 && q->moe_block_size != 48 && q->moe_block_size != 64)
+    return fail(kNotSupported, "wna16_prefill_pair: %s problem's block size %d is not 32, 48 "
+                "or 64", which, q->moe_block_size);
+  if (q->size_k % 64 != 0 || q->size_n % (swiglu ? 128 : 64) != 0)
+    return fail(kNotSupported, "wna16_prefill_pair: %s problem needs size_k %% 64 and size_n %% "
+                "%d == 0 (k=%d n=%d)", which, swiglu ? 128 : 64, q->size_k, q->size_n);
+  if (swiglu && q->mul_topk_weights)
+    return fail(kInvalidValue, "wna16_prefill_pair: %s problem: the SwiGLU epilogue applies no "
+                "top-k weight", which);
+  const void* out = swiglu ? static_cast<const void*>(q->act) : q->output;
+  if ((reinterpret_cast<uintptr_t>(q->input) & 15u) != 0 ||
+      (reinterpret_cast<uintptr_t>(out) & 15u) != 0)
+    return fail(kInvalidValue, "wna16_prefill_pair: %s problem's input and output must be "
+                "16-byte aligned", which);
+  if (static_cast<long long>(q->size_m) * q->top_k > 0x7fffffffLL)
+    return fail(kInvalidValue, "wna16_prefill_pair: %s problem: size_m * top_k overflows int32",
+                which);
+  const int inter = q->size_n / 2;
+  args = GemmArgs{q->input, swiglu ? nullptr : q->output, nullptr,
+                  reinterpret_cast<const uint32_t*>(q->b_qweight), q->b_scales, nullptr,
+                  q->sorted_token_ids, q->expert_ids, q->num_tokens_post_padded,
+                  q->topk_weights, q->sorted_token_ids_len, q->moe_block_size, q->top_k,
+                  q->mul_topk_weights, q->size_m, q->size_n, q->size_k, q->local_experts, 1,
+                  nullptr, swiglu ? q->act : nullptr, swiglu ? inter : 0};
+  gx = swiglu ? ceil_div(inter / 64, 2) : ceil_div(q->size_n / 64, 4);
+  gy = ceil_div(q->sorted_token_ids_len, q->moe_block_size);
+  return kSuccess;
+}
+
+}  // namespace
+
+int wna16_prefill_pair(const pega_wna16_problem* first, const pega_wna16_problem* second,
+                       hipStream_t stream) {
+  GemmArgs a0, a1;
+  int x0, y0, x1, y1;
+  int rc = prefill_problem(first, "first", a0, x0, y0);
+  if (rc != kSuccess) return rc;
+  rc = prefill_problem(second, "second", a1, x1, y1);
+  if (rc != kSuccess) return rc;
+  const long long n0 = static_cast<long long>(x0) * y0, n1 = static_cast<long long>(x1) * y1;
+  if (n0 + n1 > 0x7fffffffLL)
+    return fail(kNotSupported, "wna16_prefill_pair: %lld workgroups exceed the grid", n0 + n1);
+  hipLaunchKernelGGL(wna16_prefill_pair_kernel, dim3(static_cast<unsigned>(n0 + n1)), dim3(256),
+                     0, stream, a0, a1, x0, static_cast<int>(n0), x1);
+  return launch_status("wna16_prefill_pair");
+}
+
 }  // namespace pega
 
 // ---------------------------------------------------------------- C ABI
@@ -1082,4 +1165,11 @@ PEGA_API int pega_wna16_w13_swiglu(const uint16_t* input, uint16_t* act, float* 
                                 sorted_token_ids_len, moe_block_size, top_k, size_m,
                                 intermediate_dim, size_k, local_experts, group_size, sm_count,
                                 stream);
+}
+
+// Two prefill-size GEMMs in one launch (no reference symbol: the reference
+// launches a layer's shared expert and its routed experts one after another).
+PEGA_API int pega_wna16_prefill_pair(const pega_wna16_problem* first,
+                                     const pega_wna16_problem* second, hipStream_t stream) {
+  return pega::wna16_prefill_pair(first, second, stream);
 }

@@ -69,7 +69,7 @@ class RoutedExperts:
 
     def forward(self, hidden: torch.Tensor, topk_idx: torch.Tensor, topk_w: torch.Tensor,
                 out_f32: torch.Tensor, combine: str = "sum", w13_timer=None,
-                reference_flow: bool = False) -> torch.Tensor:
+                reference_flow: bool = False, companion=None) -> torch.Tensor:
         """Routed-expert forward (moe_nccl.rs:152-203 order: align, W13, SwiGLU, W2
         with the top-k weight, top-k combine).  W13 and SwiGLU are one call unless
         reference_flow is set.
@@ -81,7 +81,10 @@ class RoutedExperts:
         GPUs are never read: W2 reads only local rows, and the combine skips
         non-local routes), which gives the same bits.
         `w13_timer` (optional) exposes start()/stop(mark) and is called around the
-        W13 GEMM launch so a caller can time that kernel with stream events."""
+        W13 GEMM launch so a caller can time that kernel with stream events.
+        `companion` (optional, prefill block sizes only): a (W13, W2) pair of
+        independent problems (ExpertFFN.pair_problems, a shared expert) that run in
+        the same two launches as this layer's W13 and W2, dispatched first."""
         T = hidden.shape[0]
         rows = T * self.topk
         routing = ops.moe_align_block_size(self.route_ws, topk_idx, T, T, self.global_start)
@@ -92,7 +95,13 @@ class RoutedExperts:
         if reference_flow:
             w13_out.zero_()
         mark = w13_timer.start() if w13_timer is not None else None
-        if not reference_flow:
+        if companion is not None:
+            assert not reference_flow and self.block_size > 16
+            ops.wna16_prefill_pair(companion[0], ops.wna16_problem(
+                routing, hidden, self.w13, top_k=self.topk, size_m=T, act=act))
+            if w13_timer is not None:
+                w13_timer.stop(mark)
+        elif not reference_flow:
             # SwiGLU in the W13 epilogue (gate and up tiles in one workgroup), routed rows
             # only, same bits as W13 then SwiGLU
             ops.wna16_w13_swiglu(self.gemm_ws, routing, hidden, self.w13, act, top_k=self.topk,
@@ -108,8 +117,13 @@ class RoutedExperts:
         weighted_in_gemm = combine == "sum"
         if reference_flow:
             route_out.zero_()
-        ops.wna16_gemm(self.gemm_ws, routing, act, self.w2, topk_w, route_out, top_k=1,
-                       mul_topk_weights=weighted_in_gemm, size_m=rows)
+        if companion is not None:
+            ops.wna16_prefill_pair(companion[1], ops.wna16_problem(
+                routing, act, self.w2, top_k=1, size_m=rows, output=route_out,
+                topk_weight=topk_w, mul_topk_weights=weighted_in_gemm))
+        else:
+            ops.wna16_gemm(self.gemm_ws, routing, act, self.w2, topk_w, route_out, top_k=1,
+                           mul_topk_weights=weighted_in_gemm, size_m=rows)
         if reference_flow:
             if weighted_in_gemm:
                 ops.kimi_marlin_sum_topk_rows_f32(route_out, T, out_f32, self.topk, self.H)
@@ -186,6 +200,18 @@ class ExpertFFN:
         self.down.forward(self.act[:rows], y)
         return y
 
+    def pair_problems(self, x: torch.Tensor, y: torch.Tensor):
+        """This expert's W13 (+ SwiGLU) and W2 as problems for ops.wna16_prefill_pair
+        (prefill block sizes): the same GEMMs, and bits, as forward(x, y)."""
+        rows = x.shape[0]
+        for d in (self.up, self.down):
+            if d._routed_rows != rows:
+                d.route(rows)
+        act = self.act[:rows]
+        return (ops.wna16_problem(self.up.routing, x, self.up.w, top_k=1, size_m=rows, act=act),
+                ops.wna16_problem(self.down.routing, act, self.down.w, top_k=1, size_m=rows,
+                                  output=y))
+
 
 class Dsv2MoeLayer:
     """DeepSeek-V2-Lite-shaped MoE: softmax top-k routed experts (weights applied
@@ -200,16 +226,34 @@ class Dsv2MoeLayer:
         self.topk_idx = torch.zeros(T, routed.topk, dtype=torch.int32, device=device)
         self.routed_f32 = torch.zeros(T, H, dtype=torch.float32, device=device)
         self.shared_out = torch.zeros(T, H, dtype=torch.bfloat16, device=device)
-        # the shared expert's stream (default priority, like every stream here)
-        self.side = torch.cuda.Stream(device=device) if overlap_shared else None
+        self.overlap_shared = overlap_shared
+        # prefill block sizes overlap in shared launches; the decode kernels use a
+        # second stream (default priority, like every stream here), made on first use
+        self.pair = (overlap_shared and routed.block_size > 16 and shared.up.block_size > 16
+                     and shared.down.block_size > 16)
+        self.side = None
+        self.device = device
 
     def forward(self, hidden: torch.Tensor, logits: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
         """The shared expert does not depend on the routed branch, so by default it
-        runs on a second stream: its few large workgroups (one expert, 512 rows)
-        share the GPU with the routed kernels instead of running after them.  The
-        streams join before the add; the kernels and their bits are the same."""
+        overlaps with it: its few large workgroups (one expert, 512 rows) share the
+        GPU with the routed ones instead of running after them.  At prefill block
+        sizes each of its two GEMMs goes into the routed GEMM's launch (one stream,
+        its workgroups dispatched first); at decode sizes it runs on a second
+        stream that joins before the add.  Either way the kernels' bits are those
+        of the serial order."""
         T = hidden.shape[0]
+        if self.pair:
+            companion = self.shared.pair_problems(hidden, self.shared_out[:T])
+            ops.dsv2_router_select(logits, self.topk_w[:T], self.topk_idx[:T], T,
+                                   self.routed.topk)
+            self.routed.forward(hidden, self.topk_idx[:T], self.topk_w[:T], self.routed_f32[:T],
+                                combine="weighted", companion=companion)
+            ops.kimi_add_f32_bf16_to_bf16(self.routed_f32[:T], self.shared_out[:T], out)
+            return out
         main = torch.cuda.current_stream()
+        if self.overlap_shared and self.side is None:
+            self.side = torch.cuda.Stream(device=self.device)
         if self.side is not None:
             self.side.wait_stream(main)
             with torch.cuda.stream(self.side):

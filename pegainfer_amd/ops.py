@@ -13,6 +13,7 @@ pegainfer_amd._lib.KernelError carrying pegainfer_kernels_last_error().
 """
 from __future__ import annotations
 
+import ctypes
 import dataclasses
 import enum
 
@@ -439,6 +440,45 @@ def wna16_w13_swiglu(workspace: KimiMarlinWna16Workspace, routing: KimiMarlinRou
               _ptr(routing.expert_ids), _ptr(routing.num_tokens_post_padded),
               routing.sorted_token_ids.numel(), routing.block_size, top_k, size_m, inter,
               weight.in_dim, weight.local_experts, 32, 0, _stream())
+
+
+def wna16_problem(routing: KimiMarlinRouting, input: torch.Tensor, weight: MarlinInt4Weight, *,
+                  top_k: int, size_m: int, output: torch.Tensor = None, act: torch.Tensor = None,
+                  topk_weight: torch.Tensor = None,
+                  mul_topk_weights: bool = False) -> "_lib.Wna16Problem":
+    """One prefill-size GEMM for wna16_prefill_pair: as wna16_gemm (output) or
+    wna16_w13_swiglu (act).  The struct holds raw pointers: the tensors must
+    stay alive until the launch."""
+    _ensure((output is None) != (act is None), "give exactly one of output and act")
+    _ensure(routing.block_size > 16, f"block size {routing.block_size}: the pair launch runs "
+            "the prefill tile kernel (block sizes 32, 48, 64)")
+    size_n, size_k = weight.out_dim, weight.in_dim
+    _ensure(_is_bf16(input) and input.numel() >= size_m * size_k, "input must be bf16 [size_m, K]")
+    if act is not None:
+        _ensure(not mul_topk_weights, "the SwiGLU epilogue applies no top-k weight")
+        _ensure(_is_bf16(act) and act.numel() >= size_m * top_k * (size_n // 2),
+                "act must be bf16 [size_m * top_k, inter]")
+    else:
+        _ensure(_is_bf16(output) and output.numel() >= size_m * top_k * size_n,
+                "output must be bf16 [size_m * top_k, N]")
+    if mul_topk_weights:
+        _ensure(topk_weight is not None and topk_weight.dtype == torch.float32,
+                "mul_topk_weights needs float32 topk weights")
+    weight.validate()
+    return _lib.Wna16Problem(
+        _ptr(input), _ptr(output) if output is not None else None,
+        _ptr(act) if act is not None else None, _ptr(weight.weight_packed_uint4b8),
+        _ptr(weight.weight_scale_permuted), _ptr(routing.sorted_token_ids),
+        _ptr(routing.expert_ids), _ptr(routing.num_tokens_post_padded),
+        _ptr(topk_weight) if topk_weight is not None else None,
+        routing.sorted_token_ids.numel(), routing.block_size, top_k, int(bool(mul_topk_weights)),
+        size_m, size_n, size_k, weight.local_experts, KIMI_K2_INT4_GROUP_SIZE)
+
+
+def wna16_prefill_pair(first: "_lib.Wna16Problem", second: "_lib.Wna16Problem") -> None:
+    """Both GEMMs in one launch (the first problem's workgroups dispatched
+    first); each output has the bits of its own single launch."""
+    _lib.call("pega_wna16_prefill_pair", ctypes.byref(first), ctypes.byref(second), _stream())
 
 
 def kimi_marlin_wna16_w13_gemm(workspace, routing, input, weight, topk_weight, output_w13):

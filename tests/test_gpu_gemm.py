@@ -272,3 +272,72 @@ def test_prefill_tile_scan_over_many_blocks(oracle):
     routes = int((idx < E).sum())
     assert routes // bs > 1024, "the case must span more than one scan slab"
     assert np.array_equal(got, ref)
+
+
+def _pair_problem(g, oracle, *, E, T, topk, bs, N, K, swiglu, mul):
+    """Random problem (weights, routing, poisoned output) for the pair entry."""
+    from pegainfer_amd import ops
+    q = g.integers(-8, 8, size=(E, N, K))
+    scale_bits = oracle.f32_to_bf16((2.0 ** g.integers(-7, -3, size=(E, N, K // 32))).astype(np.float32))
+    w, _ = _setup(E, N, K, q, scale_bits)
+    a = dev(oracle.f32_to_bf16(g.standard_normal((T, K)).astype(np.float32)))
+    idx = g.integers(0, 2 * E if E > 1 else 1, size=(T, topk)).astype(np.int32)
+    ws = ops.KimiMarlinRouteWorkspace(T, bs, topk=topk, local_experts=E)
+    routing = ops.moe_align_block_size(ws, dev(idx.reshape(-1)), T, T, 0)
+    tw = dev(g.random((T, topk)).astype(np.float32))
+    width = N // 2 if swiglu else N
+    outs = [torch.full((T * topk, width), 5.0, dtype=torch.bfloat16, device="cuda")
+            for _ in range(2)]
+    return dict(ws=ws, routing=routing, w=w, a=a, tw=tw, outs=outs, T=T, topk=topk, bs=bs, N=N,
+                swiglu=swiglu, mul=mul)
+
+
+def _single_launch(pr, out):
+    from pegainfer_amd import ops
+    gws = ops.KimiMarlinWna16Workspace(pr["ws"].max_m_blocks, pr["N"], pr["bs"])
+    if pr["swiglu"]:
+        ops.wna16_w13_swiglu(gws, pr["routing"], pr["a"], pr["w"], out, top_k=pr["topk"],
+                             size_m=pr["T"])
+    else:
+        ops.wna16_gemm(gws, pr["routing"], pr["a"], pr["w"], pr["tw"], out, top_k=pr["topk"],
+                       mul_topk_weights=pr["mul"], size_m=pr["T"])
+
+
+def _pair_struct(pr, out):
+    from pegainfer_amd import ops
+    kw = dict(act=out) if pr["swiglu"] else dict(output=out, topk_weight=pr["tw"],
+                                                 mul_topk_weights=pr["mul"])
+    return ops.wna16_problem(pr["routing"], pr["a"], pr["w"], top_k=pr["topk"], size_m=pr["T"],
+                             **kw)
+
+
+@pytest.mark.parametrize("first,second", [
+    # a shared expert's W13 + SwiGLU (one expert, every row) with routed W13 + SwiGLU
+    (dict(E=1, T=512, topk=1, bs=64, N=2 * 704, K=512, swiglu=True, mul=False),
+     dict(E=16, T=512, topk=6, bs=64, N=2 * 192, K=512, swiglu=True, mul=False)),
+    # shared W2 (long K) with routed W2 times the top-k weight
+    (dict(E=1, T=300, topk=1, bs=64, N=512, K=1024, swiglu=False, mul=False),
+     dict(E=8, T=300, topk=4, bs=32, N=512, K=256, swiglu=False, mul=True)),
+    # mixed kinds and block sizes, more workgroups in the first problem
+    (dict(E=5, T=200, topk=3, bs=48, N=1024, K=256, swiglu=False, mul=True),
+     dict(E=3, T=40, topk=2, bs=32, N=2 * 128, K=768, swiglu=True, mul=False)),
+])
+def test_prefill_pair_matches_single_launches(oracle, first, second):
+    """pega_wna16_prefill_pair runs both problems in one launch; each output has the
+    bits of its own single launch (pega_wna16_gemm / pega_wna16_w13_swiglu), and rows
+    of routes that are not local keep their contents."""
+    from pegainfer_amd import ops
+    g = np.random.default_rng(first["N"] + second["K"])
+    p0 = _pair_problem(g, oracle, **first)
+    p1 = _pair_problem(g, oracle, **second)
+    for pr in (p0, p1):
+        _single_launch(pr, pr["outs"][0])
+    s0, s1 = _pair_struct(p0, p0["outs"][1]), _pair_struct(p1, p1["outs"][1])
+    ops.wna16_prefill_pair(s0, s1)
+    ops.wna16_prefill_pair(s0, s1)  # a replay writes the same values
+    for pr, spec in ((p0, first), (p1, second)):
+        ref, got = host(pr["outs"][0]), host(pr["outs"][1])
+        assert np.array_equal(got, ref)
+        assert (ref != 0x40A0).any()
+        if spec["E"] > 1:
+            assert (ref == 0x40A0).all(axis=1).any(), "rows of other GPUs' routes keep bf16(5.0)"

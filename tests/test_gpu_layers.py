@@ -211,6 +211,13 @@ def test_c4_dsv2_layer(oracle):
                               moe_block_size=sbs, top_k=1, mul_topk_weights=False, size_m=T,
                               size_n=H, size_k=sI, threads=16)
     assert_bf16_close(sh, ref2s, what="C4 shared W2")
+    # prefill block sizes: each shared-expert GEMM runs in the routed GEMM's launch,
+    # with the bits of the serial order
+    assert moe.pair
+    serial = layer.Dsv2MoeLayer(routed, shared, overlap_shared=False)
+    out_serial = torch.zeros_like(out)
+    serial.forward(hidden_d, dev(logits), out_serial)
+    assert np.array_equal(host(out_serial), host(out))
 
 
 def test_c5_kimi_prefill_sampled(oracle):

@@ -149,6 +149,60 @@ def test_fused_w13_swiglu_rejects_bad_arguments():
     assert rc == 1                         # act is written with 16-byte stores
 
 
+def _problem(**kw):
+    from pegainfer_amd import _lib
+    f = dict(input=0x1000, output=0x1000, act=None, b_qweight=0x1000, b_scales=0x1000,
+             sorted_token_ids=0x1000, expert_ids=0x1000, num_tokens_post_padded=0x1000,
+             topk_weights=0x1000, sorted_token_ids_len=640, moe_block_size=64, top_k=1,
+             mul_topk_weights=0, size_m=512, size_n=2048, size_k=1408, local_experts=1,
+             group_size=32)
+    f.update(kw)
+    return _lib.Wna16Problem(**f)
+
+
+def test_prefill_pair_rejects_bad_arguments():
+    def call(a, b):
+        return _call("pega_wna16_prefill_pair", ctypes.byref(a) if a is not None else None,
+                     ctypes.byref(b) if b is not None else None, NULL)
+    ok = _problem()
+    assert call(None, ok)[0] == 1
+    assert call(ok, None)[0] == 1
+    assert call(ok, _problem(moe_block_size=16))[0] == 801   # decode sizes: other kernels
+    assert call(_problem(moe_block_size=24), ok)[0] == 801
+    assert call(ok, _problem(input=0x1008))[0] == 1           # 16-byte aligned input
+    assert call(ok, _problem(act=0x1000, mul_topk_weights=1))[0] == 1  # no weight with SwiGLU
+    assert call(ok, _problem(act=0x1000, size_n=2048 + 64))[0] == 801  # gate/up 64-col tiles
+    assert call(ok, _problem(output=None))[0] == 1
+    assert call(ok, _problem(mul_topk_weights=1, topk_weights=None))[0] == 1
+    assert call(ok, _problem(group_size=64))[0] == 1
+    rc, reason = call(ok, _problem(size_k=1400))
+    assert rc == 801 and "second" in reason
+
+
+def test_problem_struct_matches_the_header(tmp_path):
+    """The ctypes mirror of pega_wna16_problem has the C layout: gcc compiles the
+    header and prints sizeof and every offsetof."""
+    import shutil
+    import subprocess
+    from pegainfer_amd import _lib
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not available")
+    names = [f[0] for f in _lib.Wna16Problem._fields_]
+    src = tmp_path / "layout.c"
+    src.write_text("#include <stddef.h>\n#include <stdio.h>\n#include \"pega_moe.h\"\n"
+                   "int main(void) {\n  printf(\"%zu\\n\", sizeof(pega_wna16_problem));\n" +
+                   "".join(f"  printf(\"%zu\\n\", offsetof(pega_wna16_problem, {n}));\n"
+                           for n in names) + "  return 0;\n}\n")
+    exe = tmp_path / "layout"
+    subprocess.run([gcc, "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)],
+                   check=True)
+    got = [int(x) for x in subprocess.run([str(exe)], check=True, capture_output=True,
+                                          text=True).stdout.split()]
+    assert got[0] == ctypes.sizeof(_lib.Wna16Problem) == 112
+    assert got[1:] == [getattr(_lib.Wna16Problem, n).offset for n in names]
+
+
 # ------------------------------------------------------------- Python mirror logic
 def test_manifest_shapes_match_reference_unit_tests():
     from pegainfer_amd import ops
