@@ -158,7 +158,9 @@ def bench_c3(torch, args, results):
     touched = np.unique(idx[idx < E]).size
     local_routes = int((idx < E).sum())
     alg_bytes = (touched * (W13_BYTES_PER_EXPERT + W2_BYTES_PER_EXPERT) + T * H * 2 + T * H * 4)
-    w13_bytes = touched * W13_BYTES_PER_EXPERT + T * H * 2 + local_routes * 2 * I * 2
+    # W13 + SwiGLU: weights and scales of the touched experts, the tokens' activations
+    # in, the routed rows' SwiGLU activations out
+    w13_bytes = touched * W13_BYTES_PER_EXPERT + T * H * 2 + local_routes * I * 2
     log(f"C3: block size {bs}, {touched} experts touched, {local_routes} local routes, "
         f"{alg_bytes / 1e6:.1f} MB algorithmic")
     # Eager launches, W13 timed with events on its stream (the roofline kernel).
