@@ -70,3 +70,23 @@ def test_fuse_w13_vs_oracle(oracle):
     assert np.array_equal(direct, ref_w)
     direct_s = oracle.marlin_reorder_scale(cat_s.reshape(-1), K, 2 * I, E)
     assert np.array_equal(direct_s, ref_s)
+
+
+def test_checkpoint_loader_gives_the_packed_layout(tmp_path):
+    """checkpoint.load_routed_experts (safetensors shards -> W13/W2 device packages)
+    equals packing the same experts' arrays directly, bit for bit."""
+    from ckpt_helpers import write_checkpoint
+    from pegainfer_amd import checkpoint, layer
+    truth = write_checkpoint(str(tmp_path), experts=8, inter=128, hidden=256)
+    w13, w2 = checkpoint.load_routed_experts(str(tmp_path), 3, 1, local_experts=4,
+                                             global_experts=8, hidden=256, inter=128)
+    stack = lambda proj: tuple(np.stack([truth[(e, proj)][i] for e in range(4, 8)])  # noqa: E731
+                               for i in (0, 1))
+    ref13 = layer.package_w13(stack("gate_proj"), stack("up_proj"))
+    ref2 = layer.package_projection(*stack("down_proj"))
+    for got, ref in ((w13, ref13), (w2, ref2)):
+        assert (got.local_experts, got.in_dim, got.out_dim) == (ref.local_experts, ref.in_dim,
+                                                                ref.out_dim)
+        assert torch.equal(got.weight_packed_uint4b8, ref.weight_packed_uint4b8)
+        assert torch.equal(got.weight_scale_permuted.view(torch.int16),
+                           ref.weight_scale_permuted.view(torch.int16))
