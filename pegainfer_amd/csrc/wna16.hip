@@ -890,6 +890,13 @@ __global__ void w13_swiglu_partials_kernel(GemmArgs p, uint16_t* __restrict__ ac
 
 bool valid_block_size(int bs) { return bs == 8 || (bs >= 16 && bs <= 64 && bs % 16 == 0); }
 
+// The kernels address one expert's weights and the activations through
+// 32-bit buffer ranges.  The activation range must also stay at or below
+// 2^31 bytes: offset 0x80000000 is how rows not routed here read zeros.
+bool ranges_fit(long long size_m, long long size_n, long long size_k) {
+  return size_n * size_k / 2 <= 0xffffffffLL && size_m * size_k * 2 <= 0x80000000LL;
+}
+
 }  // namespace
 
 int wna16_gemm(const uint16_t* input, uint16_t* output, float* c_tmp, long long c_tmp_len,
@@ -917,6 +924,9 @@ int wna16_gemm(const uint16_t* input, uint16_t* output, float* c_tmp, long long 
     return fail(kInvalidValue, "wna16_gemm: input and output must be 16-byte aligned");
   if (static_cast<long long>(size_m) * top_k > 0x7fffffffLL)
     return fail(kInvalidValue, "wna16_gemm: size_m * top_k overflows int32");
+  if (!ranges_fit(size_m, size_n, size_k))
+    return fail(kNotSupported, "wna16_gemm: one expert's weights over 4 GiB or the input over "
+                "2 GiB (m=%d n=%d k=%d)", size_m, size_n, size_k);
   if (cu_count <= 0) cu_count = current_cu_count();
   if (cu_count <= 0) return fail(kInvalidValue, "wna16_gemm: no device");
 
@@ -975,6 +985,11 @@ int wna16_w13_swiglu(const uint16_t* input, uint16_t* act, float* partials, long
       (reinterpret_cast<uintptr_t>(act) & 15u) != 0 ||
       (reinterpret_cast<uintptr_t>(partials) & 15u) != 0)
     return fail(kInvalidValue, "w13_swiglu: input, act and partials must be 16-byte aligned");
+  if (static_cast<long long>(size_m) * top_k > 0x7fffffffLL)
+    return fail(kInvalidValue, "w13_swiglu: size_m * top_k overflows int32");
+  if (!ranges_fit(size_m, size_n, size_k))
+    return fail(kNotSupported, "w13_swiglu: one expert's weights over 4 GiB or the input over "
+                "2 GiB (m=%d inter=%d k=%d)", size_m, inter, size_k);
   const int max_m_blocks = ceil_div(sorted_token_ids_len, moe_block_size);
   if (max_m_blocks > 65535) return fail(kNotSupported, "w13_swiglu: too many m-blocks");
   if (moe_block_size > 16) {
@@ -1070,6 +1085,9 @@ int prefill_problem(const pega_wna16_problem* q, const char* which, GemmArgs& ar
   if (static_cast<long long>(q->size_m) * q->top_k > 0x7fffffffLL)
     return fail(kInvalidValue, "wna16_prefill_pair: %s problem: size_m * top_k overflows int32",
                 which);
+  if (!ranges_fit(q->size_m, q->size_n, q->size_k))
+    return fail(kNotSupported, "wna16_prefill_pair: %s problem: one expert's weights over 4 GiB "
+                "or the input over 2 GiB", which);
   const int inter = q->size_n / 2;
   args = GemmArgs{q->input, swiglu ? nullptr : q->output, nullptr,
                   reinterpret_cast<const uint32_t*>(q->b_qweight), q->b_scales, nullptr,

@@ -104,6 +104,23 @@ def test_gemm_rejects_reference_invalid_shapes():
     assert rc == 1  # the output rows are written with 16-byte stores
 
 
+def test_gemm_entries_reject_shapes_past_the_32_bit_ranges():
+    """One expert's weights are addressed through a 32-bit range (<= 4 GiB) and the
+    activations through one of at most 2 GiB (offset 2^31 reads zeros for rows that
+    are not routed here); larger shapes are refused before any launch."""
+    def gemm(m, n, k):
+        return _call("pega_wna16_gemm", FAKE, FAKE, FAKE, ctypes.c_longlong(0), FAKE, FAKE, FAKE,
+                     0, FAKE, FAKE, FAKE, FAKE, 4096, 64, 1, False, m, n, k, 1, 32, 256, NULL)
+    rc, reason = gemm(200_000, 4096, 7168)       # input 2.87 GB
+    assert rc == 801 and "2 GiB" in reason
+    assert gemm(1, 65536, 131072)[0] == 801      # 4.29 GB of weights per expert
+    rc = _call("pega_wna16_w13_swiglu", FAKE, FAKE, NULL, ctypes.c_longlong(0), FAKE, FAKE, FAKE,
+               FAKE, FAKE, 4096, 64, 1, 200_000, 2048, 7168, 1, 32, 256, NULL)[0]
+    assert rc == 801
+    assert _call("pega_wna16_prefill_pair", ctypes.byref(_problem()),
+                 ctypes.byref(_problem(size_m=200_000, size_k=7168)), NULL)[0] == 801
+
+
 def test_repack_and_elementwise_reject_bad_arguments():
     assert _call("kimi_marlin_int4_reorder_weight_cuda", FAKE, FAKE, 64, 64, 47, 32, NULL)[0] == 1
     assert _call("kimi_marlin_int4_reorder_weight_cuda", FAKE, FAKE, 64, 60, 48, 32, NULL)[0] == 1
