@@ -5,10 +5,13 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <atomic>
+
 namespace pega {
 namespace {
 thread_local char g_last_error[512] = "";
-int g_cu_count[64] = {0};
+// per-device CU counts, filled on first use by whichever thread gets there
+std::atomic<int> g_cu_count[64];
 }  // namespace
 
 int fail(int code, const char* fmt, ...) {
@@ -29,11 +32,14 @@ int launch_status(const char* what) {
 int current_cu_count() {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
-  if (dev < 64 && g_cu_count[dev] > 0) return g_cu_count[dev];
+  if (dev < 64) {
+    const int cached = g_cu_count[dev].load(std::memory_order_relaxed);
+    if (cached > 0) return cached;
+  }
   int cus = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
     return 0;
-  if (dev < 64) g_cu_count[dev] = cus;
+  if (dev < 64) g_cu_count[dev].store(cus, std::memory_order_relaxed);
   return cus;
 }
 
