@@ -233,26 +233,28 @@ __global__ __launch_bounds__(64 * WK * (kPair ? 2 : 1), 4) void wna16_decode_ker
   const int n_units = kPair ? (p.inter >> 6) : n_tiles;  // column units per K share
   const int split = blockIdx.x / n_units;
   const int mb = blockIdx.y;
-  int ntp = p.ntp[0];
-  if (ntp > p.sorted_len) ntp = p.sorted_len;
-  if (mb >= ntp / p.bs) return;  // whole blocks only: rows stay inside sorted_len
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int valid_limit = p.size_m * p.top_k;
+  // The block's three index loads go out together, since none depends on
+  // another: the routed total, the block's expert (mb < ceil(sorted_len / bs),
+  // the grid's row count) and its rows' route ids.
+  int sid = valid_limit;
+  if (tid < p.bs && mb * p.bs + tid < p.sorted_len) sid = p.sorted_ids[mb * p.bs + tid];
   // readfirstlane: values the compiler cannot prove wave-uniform but that are
   // (block-level loads, wave index) go to SGPRs, so buffer descriptors and
   // scalar offsets built from them need no per-lane waterfall loops.
   const int expert = __builtin_amdgcn_readfirstlane(p.expert_ids[mb]);
-  if (expert < 0 || expert >= p.num_experts) return;
+  const int ntp = min(p.ntp[0], p.sorted_len);
+  // one exit test over both values, so both loads are in flight together:
+  // whole blocks only (mb < ntp / bs: rows stay inside sorted_len), local
+  // experts only
+  if (ntp < (mb + 1) * p.bs || expert < 0 || expert >= p.num_experts) return;
 
-  const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int kw = wave % WK;    // this wave's K share
   const int half = wave / WK;  // with kPair: 0 gate tile, 1 up tile
   const int nt = blockIdx.x % n_units + (kPair ? half * (p.inter >> 6) : 0);
-  const int valid_limit = p.size_m * p.top_k;
-  if (tid < 32) {
-    int sid = valid_limit;
-    if (tid < p.bs) sid = p.sorted_ids[mb * p.bs + tid];
-    s_sid[tid] = sid;
-  }
+  if (tid < 32) s_sid[tid] = sid;
   __syncthreads();
 
   const int c = lane & 31, h = lane >> 5;
