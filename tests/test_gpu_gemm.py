@@ -274,14 +274,17 @@ def test_prefill_tile_scan_over_many_blocks(oracle):
     assert np.array_equal(got, ref)
 
 
-def _pair_problem(g, oracle, *, E, T, topk, bs, N, K, swiglu, mul):
-    """Random problem (weights, routing, poisoned output) for the pair entry."""
+def _pair_problem(g, oracle, *, E, T, topk, bs, N, K, swiglu, mul, none_local=False):
+    """Random problem (weights, routing, poisoned output) for the pair entry;
+    none_local: every route belongs to another GPU (no tile at all)."""
     from pegainfer_amd import ops
     q = g.integers(-8, 8, size=(E, N, K))
     scale_bits = oracle.f32_to_bf16((2.0 ** g.integers(-7, -3, size=(E, N, K // 32))).astype(np.float32))
     w, _ = _setup(E, N, K, q, scale_bits)
     a = dev(oracle.f32_to_bf16(g.standard_normal((T, K)).astype(np.float32)))
     idx = g.integers(0, 2 * E if E > 1 else 1, size=(T, topk)).astype(np.int32)
+    if none_local:
+        idx = idx % E + E
     ws = ops.KimiMarlinRouteWorkspace(T, bs, topk=topk, local_experts=E)
     routing = ops.moe_align_block_size(ws, dev(idx.reshape(-1)), T, T, 0)
     tw = dev(g.random((T, topk)).astype(np.float32))
@@ -321,6 +324,11 @@ def _pair_struct(pr, out):
     # mixed kinds and block sizes, more workgroups in the first problem
     (dict(E=5, T=200, topk=3, bs=48, N=1024, K=256, swiglu=False, mul=True),
      dict(E=3, T=40, topk=2, bs=32, N=2 * 128, K=768, swiglu=True, mul=False)),
+    # one problem without a single local route: its workgroups all leave at once
+    (dict(E=4, T=64, topk=2, bs=32, N=512, K=512, swiglu=False, mul=False, none_local=True),
+     dict(E=6, T=100, topk=4, bs=64, N=2 * 256, K=512, swiglu=True, mul=False)),
+    (dict(E=1, T=128, topk=1, bs=64, N=2 * 192, K=256, swiglu=True, mul=False),
+     dict(E=8, T=50, topk=8, bs=32, N=256, K=256, swiglu=False, mul=True, none_local=True)),
 ])
 def test_prefill_pair_matches_single_launches(oracle, first, second):
     """pega_wna16_prefill_pair runs both problems in one launch; each output has the
@@ -338,6 +346,9 @@ def test_prefill_pair_matches_single_launches(oracle, first, second):
     for pr, spec in ((p0, first), (p1, second)):
         ref, got = host(pr["outs"][0]), host(pr["outs"][1])
         assert np.array_equal(got, ref)
+        if spec.get("none_local"):
+            assert (got == 0x40A0).all(), "no local route: nothing is written"
+            continue
         assert (ref != 0x40A0).any()
         if spec["E"] > 1:
             assert (ref == 0x40A0).all(axis=1).any(), "rows of other GPUs' routes keep bf16(5.0)"
