@@ -237,6 +237,31 @@ def bench_c1(torch, args, results):
                          gbs=b / (ms * 1e-3) / 1e9, algorithmic_bytes=b)
     log(f"C1: {ms * 1e3:.2f} us graph-replayed ({results['c1']['gbs']:.0f} GB/s), "
         f"{eager_ms * 1e3:.2f} us eager")
+    if not args.no_cpu:
+        cpu_c1(results["c1"], packed, scales, synth.normal_bf16(synth.rng(1, 2), (1, 2560)))
+
+
+def cpu_c1(res, packed, scales, x_bits):
+    """C1 is the reference's CPU-runnable case: the oracle GEMV on the same
+    inputs, on 1 thread (best of 5 runs) and on up to 16 (best of 20)."""
+    import numpy as np
+    from oracle import oracle
+    routing = dict(sorted_token_ids=np.array([0] + [1] * 7, np.int32),
+                   expert_ids=np.zeros(1, np.int32),
+                   num_tokens_post_padded=np.array([8], np.int32))
+    kw = dict(moe_block_size=8, top_k=1, mul_topk_weights=False, size_m=1, size_n=9728,
+              size_k=2560)
+    for threads in sorted({1, min(16, os.cpu_count() or 1)}):
+        best = float("inf")
+        for _ in range(5 if threads == 1 else 20):
+            t0 = time.perf_counter()
+            oracle.wna16_gemm(x_bits, packed, scales, routing, np.ones(1, np.float32),
+                              threads=threads, **kw)
+            best = min(best, time.perf_counter() - t0)
+        res[f"cpu_us_{threads}t"] = best * 1e6
+    res["cpu_kind"] = "port"
+    log("C1 CPU (oracle): " + ", ".join(f"{v:.0f} us on {k[7:-1]} thread(s)"
+                                         for k, v in res.items() if k.startswith("cpu_us_")))
 
 
 def bench_c2(torch, args, results):
