@@ -948,8 +948,12 @@ int wna16_gemm(const uint16_t* input, uint16_t* output, float* c_tmp, long long 
     const long long wgs = est_blocks * n_tiles;
     int wk = wgs >= 4LL * cu_count ? 4 : (wgs >= 2LL * cu_count ? 8 : 16);
     while (wk > 4 && groups < wk) wk >>= 1;  // waves past the last group idle
+    // Short K with workgroups to spare (the decode W2): two waves of 32+
+    // groups each amortise the prologue and the reduction better than four
+    if (wk == 4 && groups < 4 * 32 && wgs >= 8LL * cu_count) wk = 2;
     if (max_m_blocks > 65535) return fail(kNotSupported, "wna16_gemm: too many m-blocks");
-    if (wk == 4) launch_decode<4>(args, max_m_blocks, stream);
+    if (wk == 2) launch_decode<2>(args, max_m_blocks, stream);
+    else if (wk == 4) launch_decode<4>(args, max_m_blocks, stream);
     else if (wk == 8) launch_decode<8>(args, max_m_blocks, stream);
     else launch_decode<16>(args, max_m_blocks, stream);
     return launch_status("wna16_gemm (decode)");
