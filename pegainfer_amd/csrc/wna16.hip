@@ -839,66 +839,48 @@ __global__ __launch_bounds__(256, 2) void wna16_prefill_pair_kernel(GemmArgs p0,
 // columns are the sums of the K shares' fp32 partials (share order, so the
 // result does not depend on scheduling), rounded to bf16 exactly as the W13
 // output would be, then SwiGLU as in kimi_marlin_w13_swiglu_cuda.  One thread
-// per 8 columns of a row.
+// per 2 columns of a row, and all S >= splits shares' loads are issued before
+// the first add (shares past the last re-read it and are not added), so the
+// kernel costs one memory round trip whatever the share count.
+template <int S>
 __global__ void w13_swiglu_partials_kernel(GemmArgs p, uint16_t* __restrict__ act, int inter) {
   int ntp = p.ntp[0];
   if (ntp > p.sorted_len) ntp = p.sorted_len;
-  const int per_row = inter >> 3;
+  const int per_row = inter >> 1;
   const int N = p.size_n;
   const int valid_limit = p.size_m * p.top_k;
   const long long total = static_cast<long long>(ntp) * per_row;
+  const long long share = static_cast<long long>(valid_limit) * N;
   for (long long idx = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
        idx += static_cast<long long>(gridDim.x) * blockDim.x) {
     const int pos = static_cast<int>(idx / per_row);
-    const int c8 = static_cast<int>(idx - static_cast<long long>(pos) * per_row) * 8;
+    const int c2 = static_cast<int>(idx - static_cast<long long>(pos) * per_row) * 2;
     // the row's id and its block's expert go out together
     const int sid = p.sorted_ids[pos];
     const int e = p.expert_ids[pos / p.bs];
     if (static_cast<unsigned>(sid) >= static_cast<unsigned>(valid_limit)) continue;
     if (e < 0 || e >= p.num_experts) continue;
-    float g[8] = {0, 0, 0, 0, 0, 0, 0, 0}, u[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    const float* base = p.partial + static_cast<long long>(sid) * N + c8;
-    const long long share = static_cast<long long>(valid_limit) * N;
-    auto add = [&](const float4 (&v)[4]) {
-      g[0] += v[0].x; g[1] += v[0].y; g[2] += v[0].z; g[3] += v[0].w;
-      g[4] += v[1].x; g[5] += v[1].y; g[6] += v[1].z; g[7] += v[1].w;
-      u[0] += v[2].x; u[1] += v[2].y; u[2] += v[2].z; u[3] += v[2].w;
-      u[4] += v[3].x; u[5] += v[3].y; u[6] += v[3].z; u[7] += v[3].w;
-    };
-    auto load = [&](float4 (&v)[4], int sp) {
-      const float* row = base + sp * share;
-      v[0] = *reinterpret_cast<const float4*>(row);
-      v[1] = *reinterpret_cast<const float4*>(row + 4);
-      v[2] = *reinterpret_cast<const float4*>(row + inter);
-      v[3] = *reinterpret_cast<const float4*>(row + inter + 4);
-    };
-    // four shares' loads in flight at a time, summed in share order
-    int sp = 0;
-    for (; sp + 4 <= p.splits; sp += 4) {
-      float4 v0[4], v1[4], v2[4], v3[4];
-      load(v0, sp);
-      load(v1, sp + 1);
-      load(v2, sp + 2);
-      load(v3, sp + 3);
-      add(v0);
-      add(v1);
-      add(v2);
-      add(v3);
-    }
-    for (; sp < p.splits; ++sp) {
-      float4 v[4];
-      load(v, sp);
-      add(v);
-    }
-    uint32_t w[4];
+    const float* base = p.partial + static_cast<long long>(sid) * N + c2;
+    float2 gv[S], uv[S];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint16_t lo = swiglu_one(bf2f(f2bf(g[2 * i])), bf2f(f2bf(u[2 * i])));
-      const uint16_t hi = swiglu_one(bf2f(f2bf(g[2 * i + 1])), bf2f(f2bf(u[2 * i + 1])));
-      w[i] = static_cast<uint32_t>(lo) | (static_cast<uint32_t>(hi) << 16);
+    for (int sp = 0; sp < S; ++sp) {
+      const long long off = static_cast<long long>(min(sp, p.splits - 1)) * share;
+      gv[sp] = *reinterpret_cast<const float2*>(base + off);
+      uv[sp] = *reinterpret_cast<const float2*>(base + off + inter);
     }
-    *reinterpret_cast<uint4*>(act + static_cast<long long>(sid) * inter + c8) =
-        make_uint4(w[0], w[1], w[2], w[3]);
+    float g0 = 0.0f, g1 = 0.0f, u0 = 0.0f, u1 = 0.0f;
+#pragma unroll
+    for (int sp = 0; sp < S; ++sp) {
+      // a select, not a branch: the loads above stay ahead of every add
+      const bool use = sp < p.splits;
+      g0 = use ? g0 + gv[sp].x : g0;
+      g1 = use ? g1 + gv[sp].y : g1;
+      u0 = use ? u0 + uv[sp].x : u0;
+      u1 = use ? u1 + uv[sp].y : u1;
+    }
+    const uint32_t lo = swiglu_one(bf2f(f2bf(g0)), bf2f(f2bf(u0)));
+    const uint32_t hi = swiglu_one(bf2f(f2bf(g1)), bf2f(f2bf(u1)));
+    *reinterpret_cast<uint32_t*>(act + static_cast<long long>(sid) * inter + c2) = lo | (hi << 16);
   }
 }
 
@@ -1061,11 +1043,16 @@ int wna16_w13_swiglu(const uint16_t* input, uint16_t* act, float* partials, long
   else launch_decode<16>(args, max_m_blocks, stream);
   const int rc = launch_status("w13_swiglu (GEMM)");
   if (rc != kSuccess) return rc;
-  const long long work = static_cast<long long>(sorted_token_ids_len) * (inter / 8);
+  const long long work = static_cast<long long>(sorted_token_ids_len) * (inter / 2);
   long long grid = (work + 255) / 256;
   if (grid > 4LL * cu_count) grid = 4LL * cu_count;
-  hipLaunchKernelGGL(w13_swiglu_partials_kernel, dim3(static_cast<unsigned>(grid)), dim3(256), 0,
-                     stream, args, act, inter);
+  const dim3 g(static_cast<unsigned>(grid));
+  if (splits <= 4)
+    hipLaunchKernelGGL(w13_swiglu_partials_kernel<4>, g, dim3(256), 0, stream, args, act, inter);
+  else if (splits <= 8)
+    hipLaunchKernelGGL(w13_swiglu_partials_kernel<8>, g, dim3(256), 0, stream, args, act, inter);
+  else
+    hipLaunchKernelGGL(w13_swiglu_partials_kernel<16>, g, dim3(256), 0, stream, args, act, inter);
   return launch_status("w13_swiglu (SwiGLU)");
 }
 
