@@ -226,6 +226,20 @@ int kimi_residual_add_scaled_bf16_cuda(const uint16_t* hidden, const uint16_t* p
 int kimi_add_f32_bf16_to_bf16_cuda(const float* a, const uint16_t* b, uint16_t* out, int n,
                                    hipStream_t stream);
 
+/* ---------------- dense bf16 GEMM (shared expert) ----------------
+ * Y[n][m] = bf16(sum_k W[m][k] * X[n][k]) with fp32 accumulation; W [M][K],
+ * X [N][K], Y [N][M] bf16 row-major (the reference's cublasGemmEx(OP_T, OP_N)
+ * call, pegainfer-kernels/csrc/shared/linear.cu:321-344).  Needs M % 16 == 0,
+ * K % 32 == 0 and 16-byte aligned W and X (801 otherwise).  Never allocates. */
+
+/* Replaces gemm_cuda, pegainfer-kernels/src/ffi/shared.rs:220-228. */
+int gemm_cuda(const uint16_t* W, const uint16_t* X, uint16_t* Y, int M, int N, int K,
+              hipStream_t stream);
+
+/* Replaces gemm_graphsafe_cuda, pegainfer-kernels/src/ffi/shared.rs:230-238. */
+int gemm_graphsafe_cuda(const uint16_t* W, const uint16_t* X, uint16_t* Y, int M, int N, int K,
+                        hipStream_t stream);
+
 /* ---------------- routing select ---------------- */
 
 /* No reference symbol of its own: the select stage (sigmoid, top-k of score+bias, renormalise)

@@ -387,6 +387,42 @@ int oracle_swiglu(const uint16_t *w13, uint16_t *out, int rows, int inter) {
   return 0;
 }
 
+/* ------------------------------------------------------------------------ */
+/* Dense bf16 GEMM of the shared expert (pegainfer-kernels/csrc/shared/      */
+/* linear.cu:321-344, gemm_graphsafe_cuda: cublasGemmEx(OP_T, OP_N, M, N, K,  */
+/* W lda K, X ldb K, Y ldc M, CUBLAS_COMPUTE_32F), called from               */
+/* pegainfer-kimi-k2/src/runner/moe_nccl.rs:107-123):                         */
+/*   Y[n][m] = bf16( sum_k f(W[m][k]) * f(X[n][k]) ),  fp32 accumulation     */
+/* (k ascending here; the library's order is its own, so parity is to the    */
+/* tolerance).  W [M][K], X [N][K], Y [N][M], all bf16 row-major.            */
+/* Pinned by: small-integer operands with power-of-two scales (every partial */
+/* sum exact, so any order gives these bits), one-hot rows of X (Y equals a  */
+/* column of W), zero W, and fp64 brute force on random operands within the */
+/* fp32-accumulation bound.                                                 */
+/* ------------------------------------------------------------------------ */
+int oracle_dense_gemm(const uint16_t *W, const uint16_t *X, uint16_t *Y, int M, int N, int K) {
+  if (M <= 0 || N <= 0 || K <= 0) return 1;
+  float *wrow = (float *)malloc(sizeof(float) * (size_t)K);
+  float *xrow = (float *)malloc(sizeof(float) * (size_t)K);
+  if (!wrow || !xrow) {
+    free(wrow);
+    free(xrow);
+    return 2;
+  }
+  for (int n = 0; n < N; ++n) {
+    for (int k = 0; k < K; ++k) xrow[k] = bf(X[(size_t)n * K + k]);
+    for (int m = 0; m < M; ++m) {
+      for (int k = 0; k < K; ++k) wrow[k] = bf(W[(size_t)m * K + k]);
+      float acc = 0.0f;
+      for (int k = 0; k < K; ++k) acc += wrow[k] * xrow[k];
+      Y[(size_t)n * M + m] = to_bf(acc);
+    }
+  }
+  free(wrow);
+  free(xrow);
+  return 0;
+}
+
 /* K4: top-k row sum (kimi_marlin_wna16.cu:392-408): fp32, k ascending from 0.
  * Pinned by: numpy float32 sequential accumulation. */
 int oracle_sum_topk_rows(const uint16_t *route_output, float *out, int active_tokens,

@@ -44,6 +44,7 @@ def lib():
             "oracle_marlin_fuse_w13": [_P] * 6 + [_I] * 4,
             "oracle_wna16_gemm": [_P] * 8 + [_I] * 9,
             "oracle_swiglu": [_P, _P, _I, _I],
+            "oracle_dense_gemm": [_P, _P, _P, _I, _I, _I],
             "oracle_sum_topk_rows": [_P, _P, _I, _I, _I],
             "oracle_residual_add_scaled_f32": [_P, _P, _P, _F, _P, _I],
             "oracle_residual_add_scaled_bf16": [_P, _P, _P, _F, _P, _I],
@@ -192,6 +193,20 @@ def wna16_gemm(input_bf16, qweight_ckpt_u8, scales_ckpt_bf16, routing, topk_weig
         ei.size, moe_block_size, top_k, int(bool(mul_topk_weights)), size_m, size_n, size_k,
         group_size, threads), "wna16_gemm")
     return output
+
+
+# ---------------------------------------------------------------- dense GEMM
+def dense_gemm(w_bf16, x_bf16):
+    """Y[n][m] = bf16(sum_k W[m][k] X[n][k]) with fp32 accumulation (the shared
+    expert's bf16 GEMM, linear.cu:321-344); W [M, K], X [N, K] -> Y [N, M]."""
+    w = np.ascontiguousarray(w_bf16, dtype=np.uint16)
+    x = np.ascontiguousarray(x_bf16, dtype=np.uint16)
+    M, K = w.shape
+    N = x.shape[0]
+    assert x.shape[1] == K
+    y = np.empty((N, M), np.uint16)
+    _check(lib().oracle_dense_gemm(_ptr(w), _ptr(x), _ptr(y), M, N, K), "dense_gemm")
+    return y
 
 
 # ---------------------------------------------------------------- elementwise

@@ -57,6 +57,8 @@ SIGNATURES = {
     "pega_kimi_router_select": [_P, _P, _P, _P, _I, _I, _I, _F, _P],
     "pega_dsv2_router_select": [_P, _P, _P, _I, _I, _I, _P],
     "pega_wna16_prefill_pair": [ctypes.POINTER(Wna16Problem), ctypes.POINTER(Wna16Problem), _P],
+    "gemm_cuda": [_P, _P, _P, _I, _I, _I, _P],
+    "gemm_graphsafe_cuda": [_P, _P, _P, _I, _I, _I, _P],
 }
 _RESTYPE = {"pegainfer_kernels_last_error": ctypes.c_char_p}
 

@@ -1,0 +1,199 @@
+// Dense bf16 GEMM of the shared expert on MI355X (gfx950):
+//
+//   Y[n][m] = bf16( sum_k f(W[m][k]) * f(X[n][k]) ),  fp32 accumulation,
+//   W [M][K], X [N][K], Y [N][M], bf16 row-major
+//
+// Reference: pegainfer-kernels/csrc/shared/linear.cu:321-344
+// (gemm_graphsafe_cuda: cublasGemmEx(OP_T, OP_N, M, N, K, W lda K, X ldb K,
+// Y ldc M, CUBLAS_COMPUTE_32F)), bound in pegainfer-kernels/src/ffi/shared.rs:220-238
+// and called for the Kimi shared expert's gate/up and down projections
+// (pegainfer-kimi-k2/src/runner/moe_nccl.rs:107-123).
+//
+// The decode-sized token counts this serves make the GEMM a weight stream, so
+// one workgroup owns 16 output features for up to 64 tokens and reads its W
+// rows from HBM exactly once; its WK waves split K and are reduced through
+// LDS in wave order (deterministic).  Per 32-k step a lane issues one 16-byte
+// load of W (row m0 + c, k 8q..8q+7: the B fragment of a 16x16x32 MFMA, no
+// transpose) and one 16-byte load of X per 16-token row block (the A
+// fragment), then one v_mfma_f32_16x16x32_bf16 per row block.  A and B take
+// the same k slots per lane, so the product is exact whatever k order the
+// MFMA assigns to them.  Token rows past N read zeros through an
+// out-of-range buffer offset and are never stored.
+#include "common.h"
+#include "pega_moe.h"
+
+namespace pega {
+namespace {
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float floatx4_t;
+typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4_t;
+
+constexpr uint32_t kOutOfRange = 0x80000000u;  // voffset that fails every range check
+constexpr int kCached = 0;
+constexpr int kStream = 2;  // non-temporal: W is read exactly once per launch
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
+                                           static_cast<int>(bytes), 0x00020000);
+}
+
+template <int kPolicy>
+__device__ __forceinline__ u32x4_t load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(voff), static_cast<int>(soff),
+                                               kPolicy);
+}
+
+template <int RB>
+struct StepRegs {
+  u32x4_t w;      // B fragment: W[m0 + c][k0 + 8q .. +7]
+  u32x4_t x[RB];  // A fragments: X[n0 + 16 rb + c][k0 + 8q .. +7]
+};
+
+// One workgroup per (16 output features, 16 RB tokens); WK waves split the
+// K/32 steps; D steps per wave in flight.
+template <int WK, int RB>
+__global__ __launch_bounds__(64 * WK) void dense_gemm_kernel(const uint16_t* __restrict__ W,
+                                                             const uint16_t* __restrict__ X,
+                                                             uint16_t* __restrict__ Y, int M,
+                                                             int N, int K) {
+  constexpr int D = 4;
+  __shared__ float s_red[WK][RB * 4][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c = lane & 15, q = lane >> 4;
+  const int m0 = blockIdx.x * 16;
+  const int n0 = blockIdx.y * (16 * RB);
+  const int steps = K >> 5;
+  const int s0 = (steps * wave) / WK, s1 = (steps * (wave + 1)) / WK;
+
+  const __amdgpu_buffer_rsrc_t wr =
+      make_rsrc(W + static_cast<long long>(m0) * K, 16u * static_cast<uint32_t>(K) * 2u);
+  const uint32_t w_voff = (static_cast<uint32_t>(c) * K + 8u * q) * 2u;
+  const __amdgpu_buffer_rsrc_t xr =
+      make_rsrc(X, static_cast<uint32_t>(N) * static_cast<uint32_t>(K) * 2u);
+  uint32_t x_voff[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    const int n = n0 + 16 * rb + c;
+    x_voff[rb] = n < N ? (static_cast<uint32_t>(n) * K + 8u * q) * 2u : kOutOfRange;
+  }
+
+  auto load_step = [&](StepRegs<RB>& r, int s) {
+    s = min(max(s, 0), steps - 1);  // every scalar offset stays inside the rows
+    const uint32_t soff = static_cast<uint32_t>(s) * 64u;
+    r.w = load16<kStream>(wr, w_voff, soff);
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) r.x[rb] = load16<kCached>(xr, x_voff[rb], soff);
+  };
+  floatx4_t acc[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) acc[rb] = floatx4_t{};
+  auto compute_step = [&](const StepRegs<RB>& r) {
+    const bf16x8_t b = __builtin_bit_cast(bf16x8_t, r.w);
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+      acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, r.x[rb]), b,
+                                                         acc[rb], 0, 0, 0);
+  };
+
+  StepRegs<RB> slot[D];
+#pragma unroll
+  for (int j = 0; j < D; ++j) {
+    load_step(slot[j], s0 + j < s1 ? s0 + j : s1 - 1);
+    __builtin_amdgcn_sched_barrier(0);  // one issue order for prologue and loop
+  }
+  // Whole rounds of D steps; a slot is refilled with the step D ahead right
+  // after its compute (pinned there, so each step waits only for its own
+  // loads), clamped to the last step of the slice past its end.
+  const int rounds = (s1 - s0) / D;
+  int s = s0;
+  for (int r = 0; r < rounds; ++r, s += D) {
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      compute_step(slot[j]);
+      load_step(slot[j], min(s + j + D, s1 - 1));
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < D - 1; ++j)
+    if (s + j < s1) compute_step(slot[j]);
+
+  // Reduction over the WK waves in wave order.  Accumulator element e of row
+  // block rb holds token n0 + 16 rb + 4 q + e, feature m0 + c.
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s_red[wave][rb * 4 + e][lane] = acc[rb][e];
+  __syncthreads();
+  for (int j = wave; j < RB * 4; j += WK) {
+    float sum = 0.0f;
+#pragma unroll
+    for (int w = 0; w < WK; ++w) sum += s_red[w][j][lane];
+    const int n = n0 + 16 * (j >> 2) + 4 * q + (j & 3);
+    if (n < N) Y[static_cast<long long>(n) * M + m0 + c] = f2bf(sum);
+  }
+}
+
+template <int WK>
+void launch_dense(int rb, dim3 grid, const uint16_t* W, const uint16_t* X, uint16_t* Y, int M,
+                  int N, int K, hipStream_t stream) {
+  const dim3 block(64 * WK);
+  switch (rb) {
+    case 1: hipLaunchKernelGGL((dense_gemm_kernel<WK, 1>), grid, block, 0, stream, W, X, Y, M, N, K); break;
+    case 2: hipLaunchKernelGGL((dense_gemm_kernel<WK, 2>), grid, block, 0, stream, W, X, Y, M, N, K); break;
+    case 3: hipLaunchKernelGGL((dense_gemm_kernel<WK, 3>), grid, block, 0, stream, W, X, Y, M, N, K); break;
+    default: hipLaunchKernelGGL((dense_gemm_kernel<WK, 4>), grid, block, 0, stream, W, X, Y, M, N, K); break;
+  }
+}
+
+int dense_gemm(const uint16_t* W, const uint16_t* X, uint16_t* Y, int M, int N, int K,
+               hipStream_t stream, const char* name) {
+  if (!W || !X || !Y) return fail(kInvalidValue, "%s: null pointer", name);
+  if (M <= 0 || N <= 0 || K <= 0)
+    return fail(kInvalidValue, "%s: bad shape M=%d N=%d K=%d", name, M, N, K);
+  if (M % 16 != 0 || K % 32 != 0)
+    return fail(kNotSupported, "%s: M %% 16 and K %% 32 must be 0 (M=%d K=%d)", name, M, K);
+  if ((reinterpret_cast<uintptr_t>(W) & 15u) != 0 || (reinterpret_cast<uintptr_t>(X) & 15u) != 0)
+    return fail(kInvalidValue, "%s: W and X must be 16-byte aligned", name);
+  // X is addressed through one 32-bit buffer range that must stay below the
+  // out-of-range offset
+  if (static_cast<long long>(N) * K * 2 >= static_cast<long long>(kOutOfRange))
+    return fail(kNotSupported, "%s: X over 2 GiB (N=%d K=%d)", name, N, K);
+  const int cu = current_cu_count();
+  if (cu <= 0) return fail(kInvalidValue, "%s: no device", name);
+  const int rb = N <= 16 ? 1 : N <= 32 ? 2 : N <= 48 ? 3 : 4;
+  const dim3 grid(M / 16, ceil_div(N, 16 * rb));
+  if (grid.y > 65535u) return fail(kNotSupported, "%s: too many token blocks (N=%d)", name, N);
+  // Few workgroups: more waves each, splitting K (at least one step a wave).
+  const long long wgs = static_cast<long long>(grid.x) * grid.y;
+  int wk = wgs <= cu ? 16 : (wgs <= 2LL * cu ? 8 : 4);
+  while (wk > 1 && K / 32 < wk) wk >>= 1;
+  switch (wk) {
+    case 16: launch_dense<16>(rb, grid, W, X, Y, M, N, K, stream); break;
+    case 8: launch_dense<8>(rb, grid, W, X, Y, M, N, K, stream); break;
+    case 4: launch_dense<4>(rb, grid, W, X, Y, M, N, K, stream); break;
+    case 2: launch_dense<2>(rb, grid, W, X, Y, M, N, K, stream); break;
+    default: launch_dense<1>(rb, grid, W, X, Y, M, N, K, stream); break;
+  }
+  return launch_status(name);
+}
+
+}  // namespace
+}  // namespace pega
+
+using namespace pega;
+
+// Reference: pegainfer-kernels/src/ffi/shared.rs:220-228 (gemm_cuda) and
+// :230-238 (gemm_graphsafe_cuda); both compute the same GEMM, and this
+// library's version never allocates, so both are graph-safe.
+PEGA_API int gemm_cuda(const uint16_t* W, const uint16_t* X, uint16_t* Y, int M, int N, int K,
+                       hipStream_t stream) {
+  return dense_gemm(W, X, Y, M, N, K, stream, "gemm_cuda");
+}
+
+PEGA_API int gemm_graphsafe_cuda(const uint16_t* W, const uint16_t* X, uint16_t* Y, int M, int N,
+                                 int K, hipStream_t stream) {
+  return dense_gemm(W, X, Y, M, N, K, stream, "gemm_graphsafe_cuda");
+}

@@ -169,6 +169,57 @@ class DenseW4A16:
         return y
 
 
+class KimiSharedExpert:
+    """The Kimi-K2 shared expert, a bf16 dense MLP (moe_nccl.rs:107-123): gate/up
+    GEMM [2I, H] -> SwiGLU (gate first) -> down GEMM [H, I], bf16 `projected` out."""
+
+    def __init__(self, gate_up: torch.Tensor, down: torch.Tensor, *, max_tokens: int,
+                 device="cuda"):
+        assert gate_up.dim() == 2 and down.dim() == 2
+        self.gate_up, self.down = gate_up.contiguous(), down.contiguous()
+        self.I = gate_up.shape[0] // 2
+        self.H = gate_up.shape[1]
+        assert tuple(down.shape) == (self.H, self.I)
+        bf = dict(dtype=torch.bfloat16, device=device)
+        self.gu = torch.zeros(max_tokens, 2 * self.I, **bf)
+        self.act = torch.zeros(max_tokens, self.I, **bf)
+
+    def forward(self, normed: torch.Tensor, projected: torch.Tensor) -> torch.Tensor:
+        T = normed.shape[0]
+        ops.gemm_graphsafe(self.gate_up, normed, self.gu[:T])
+        ops.kimi_marlin_w13_swiglu(self.gu[:T], self.act[:T], T, self.I)
+        ops.gemm_graphsafe(self.down, self.act[:T], projected)
+        return projected
+
+
+class KimiMoeDecodeLayer:
+    """One GPU's Kimi-K2 MoE decode layer (moe_nccl.rs:98-239 without the
+    collectives): the shared expert on the normed input, the router select, the
+    routed experts (fp32 combine of the local routes) and the residual join
+    out = bf16(routed * 2.827 + bf16(hidden + projected)) (kimi_experts.cu:25-39)."""
+
+    def __init__(self, routed: RoutedExperts, shared: KimiSharedExpert, *, n_experts: int = 384,
+                 device="cuda"):
+        self.routed, self.shared = routed, shared
+        T, H = routed.max_tokens, routed.H
+        self.projected = torch.zeros(T, H, dtype=torch.bfloat16, device=device)
+        self.routed_f32 = torch.zeros(T, H, dtype=torch.float32, device=device)
+        self.topk_w = torch.zeros(T, routed.topk, dtype=torch.float32, device=device)
+        self.topk_idx = torch.zeros(T, routed.topk, dtype=torch.int32, device=device)
+
+    def forward(self, hidden: torch.Tensor, normed: torch.Tensor, logits: torch.Tensor,
+                bias: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+        T = hidden.shape[0]
+        projected, routed_f32 = self.projected[:T], self.routed_f32[:T]
+        self.shared.forward(normed, projected)
+        ops.kimi_router_select(logits, bias, self.topk_w[:T], self.topk_idx[:T], T,
+                               topk=self.routed.topk)
+        self.routed.forward(normed, self.topk_idx[:T], self.topk_w[:T], routed_f32)
+        ops.kimi_residual_add_scaled_f32(hidden, projected, routed_f32, ops.KIMI_K2_ROUTER_SCALE,
+                                         out)
+        return out
+
+
 class ExpertFFN:
     """One expert: W13 -> SwiGLU -> W2 (no routing weight), bf16 out."""
 

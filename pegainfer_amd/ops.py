@@ -565,6 +565,26 @@ def kimi_add_f32_bf16_to_bf16(a, b, out) -> None:
 
 
 # --------------------------------------------------------------------------
+# Dense bf16 GEMM (the shared expert's projections)
+# --------------------------------------------------------------------------
+def gemm_graphsafe(w: torch.Tensor, x: torch.Tensor, y: torch.Tensor) -> None:
+    """Y[n][m] = bf16(sum_k W[m][k] * X[n][k]) with fp32 accumulation: W [M, K]
+    (a DeviceMatrix, rows = output features), X [N, K], Y [N, M], all bf16.
+    Mirrors typed_ops.rs:296-344 (gemm_dm_typed_to_hs_graphsafe /
+    gemm_dm_hs_to_typed_graphsafe -> gemm_graphsafe_cuda)."""
+    _ensure(_is_bf16(w) and _is_bf16(x) and _is_bf16(y), "dense GEMM operands must be bf16")
+    _ensure(w.dim() == 2 and x.dim() == 2 and y.dim() == 2, "dense GEMM operands must be 2-D")
+    _ensure(w.is_contiguous() and x.is_contiguous() and y.is_contiguous(),
+            "dense GEMM operands must be contiguous")
+    M, K = w.shape
+    N = x.shape[0]
+    _ensure(x.shape[1] == K, f"DM GEMM weight cols={K} must match input dim {x.shape[1]}")
+    _ensure(tuple(y.shape) == (N, M),
+            f"DM GEMM shape mismatch: w.rows={M}, y={tuple(y.shape)}, x.seq={N}")
+    _lib.call("gemm_graphsafe_cuda", _ptr(w), _ptr(x), _ptr(y), M, N, K, _stream())
+
+
+# --------------------------------------------------------------------------
 # Routing select
 # --------------------------------------------------------------------------
 def kimi_router_select(logits: torch.Tensor, bias: torch.Tensor, topk_weight: torch.Tensor,

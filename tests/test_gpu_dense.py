@@ -1,0 +1,111 @@
+"""GPU parity of the dense bf16 GEMM (gemm_graphsafe_cuda / gemm_cuda, the
+Kimi shared expert's projections; linear.cu:321-344) and of the whole Kimi
+decode layer with its shared expert and residual join (moe_nccl.rs:98-239),
+against the CPU oracle.  Tolerance: |gpu - ref| <= 1e-3 + 1e-2 |ref| (the
+library sums K in its own order); exact where every partial sum is exact."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_helpers import assert_bf16_close, dev, host
+
+pytestmark = pytest.mark.gpu
+
+
+def _gemm(w, x):
+    from pegainfer_amd import ops
+    y = torch.zeros(x.shape[0], w.shape[0], dtype=torch.bfloat16, device="cuda")
+    ops.gemm_graphsafe(dev(w), dev(x), y)
+    return host(y)
+
+
+@pytest.mark.parametrize("M,N,K", [(4096, 64, 7168), (7168, 64, 2048), (64, 1, 32),
+                                   (48, 7, 96), (256, 33, 512), (128, 100, 256), (16, 200, 64),
+                                   (2048, 17, 1024)])
+def test_dense_gemm_matches_oracle(oracle, M, N, K):
+    g = np.random.default_rng(M * 131 + N * 7 + K)
+    w = oracle.f32_to_bf16((g.standard_normal((M, K)) * 0.02).astype(np.float32))
+    x = oracle.f32_to_bf16(g.standard_normal((N, K)).astype(np.float32))
+    assert_bf16_close(_gemm(w, x), oracle.dense_gemm(w, x), what=f"dense {M}x{N}x{K}")
+
+
+def test_dense_gemm_exact_when_partial_sums_are_exact(oracle):
+    g = np.random.default_rng(3)
+    M, N, K = 96, 40, 640
+    w = oracle.f32_to_bf16(np.ldexp(g.integers(-8, 8, (M, K)), g.integers(-4, 2, (M, K)))
+                           .astype(np.float32))
+    x = oracle.f32_to_bf16(g.integers(-6, 7, (N, K)).astype(np.float32))
+    assert np.array_equal(_gemm(w, x), oracle.dense_gemm(w, x))
+
+
+def test_dense_gemm_one_hot_rows_give_weight_columns(oracle):
+    g = np.random.default_rng(4)
+    M, K = 160, 256
+    w = oracle.f32_to_bf16(g.standard_normal((M, K)).astype(np.float32))
+    ks = [0, 31, 32, 200, 255]
+    x = np.zeros((len(ks), K), np.uint16)
+    for n, k in enumerate(ks):
+        x[n, k] = 0x3F80  # bf16 1.0
+    y = _gemm(w, x)
+    for n, k in enumerate(ks):
+        assert np.array_equal(y[n], w[:, k])
+
+
+def test_dense_gemm_entry_points_agree_and_reject(oracle):
+    from pegainfer_amd import _lib
+    g = np.random.default_rng(5)
+    M, N, K = 64, 9, 128
+    w = dev(oracle.f32_to_bf16(g.standard_normal((M, K)).astype(np.float32)))
+    x = dev(oracle.f32_to_bf16(g.standard_normal((N, K)).astype(np.float32)))
+    y1 = torch.zeros(N, M, dtype=torch.bfloat16, device="cuda")
+    y2 = torch.zeros_like(y1)
+    L = _lib.lib()
+    s = torch.cuda.current_stream().cuda_stream
+    p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    assert L.gemm_cuda(p(w), p(x), p(y1), M, N, K, s) == 0
+    assert L.gemm_graphsafe_cuda(p(w), p(x), p(y2), M, N, K, s) == 0
+    assert np.array_equal(host(y1), host(y2))
+    assert L.gemm_graphsafe_cuda(p(w), p(x), p(y2), 40, N, K, s) == 801    # M % 16
+    assert L.gemm_graphsafe_cuda(p(w), p(x), p(y2), M, N, 100, s) == 801   # K % 32
+    assert L.gemm_graphsafe_cuda(None, p(x), p(y2), M, N, K, s) == 1
+    assert L.gemm_graphsafe_cuda(p(w), p(x), p(y2), M, 0, K, s) == 1
+
+
+def test_kimi_decode_layer_with_shared_expert(oracle):
+    """Shared expert (bf16 gate/up and down), router select, routed experts and
+    the residual join, against the oracle's chain of the same stages."""
+    from pegainfer_amd import layer, ops, synth
+    E, H, I, T, SI = 48, 1024, 256, 24, 512
+    g = synth.rng(11, 1)
+    gate, up, down = (synth.int4_checkpoint(g, E, I, H), synth.int4_checkpoint(g, E, I, H),
+                      synth.int4_checkpoint(g, E, H, I))
+    gu = oracle.f32_to_bf16((g.standard_normal((2 * SI, H)) * 0.03).astype(np.float32))
+    dn = oracle.f32_to_bf16((g.standard_normal((H, SI)) * 0.03).astype(np.float32))
+    hidden = synth.normal_bf16(g, (T, H))
+    normed = synth.normal_bf16(g, (T, H))
+    logits = g.standard_normal((T, 384), dtype=np.float32)
+    bias = np.zeros(384, np.float32)
+    routed = layer.RoutedExperts(layer.package_w13(gate, up), layer.package_projection(*down),
+                                 max_tokens=T, topk=8, block_size=ops.kimi_marlin_block_size(T))
+    shared = layer.KimiSharedExpert(dev(gu), dev(dn), max_tokens=T)
+    moe = layer.KimiMoeDecodeLayer(routed, shared)
+    out = torch.zeros(T, H, dtype=torch.bfloat16, device="cuda")
+    moe.forward(dev(hidden), dev(normed), dev(logits), dev(bias), out)
+    # the oracle's chain
+    idx, w = oracle.kimi_router(logits, bias, 8, 1.0)
+    assert np.array_equal(host(moe.topk_idx), idx)
+    proj = oracle.dense_gemm(dn, oracle.swiglu(oracle.dense_gemm(gu, normed), SI))
+    assert_bf16_close(host(moe.projected), proj, what="shared expert projected")
+    w13p = np.concatenate([gate[0], up[0]], axis=1)
+    w13s = np.concatenate([gate[1], up[1]], axis=1)
+    routed_ref, _ = oracle.kimi_moe_layer(normed, w13p, w13s, down[0], down[1], idx.reshape(-1),
+                                          w, global_start=0, local_experts=E,
+                                          block_size=routed.block_size, hidden=H, inter=I)
+    ref = oracle.residual_add_scaled_f32(hidden, proj, routed_ref, ops.KIMI_K2_ROUTER_SCALE)
+    # two GEMM chains of the same tolerance composed: twice the per-GEMM bound
+    assert_bf16_close(host(out), ref, rtol=2e-2, atol=2e-3, what="Kimi decode layer")
+    # the join itself is exact given its inputs
+    assert np.array_equal(host(out), oracle.residual_add_scaled_f32(
+        hidden, host(moe.projected), host(moe.routed_f32), ops.KIMI_K2_ROUTER_SCALE))

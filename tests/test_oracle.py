@@ -404,3 +404,46 @@ def test_kimi_layer_composite_small(oracle):
                 got = oracle.bf16_to_f32(w13[r])
                 assert np.allclose(got, exact, rtol=2 ** -7, atol=1e-6)
     assert routed.shape == (T, H) and np.isfinite(routed).all()
+
+
+# ---------------------------------------------------------------- dense bf16 GEMM
+# (the shared expert's projections, linear.cu:321-344)
+def test_dense_gemm_exact_small_integers(oracle):
+    # small integers times powers of two: every partial sum is exact, so any
+    # summation order gives these bits; checked against an fp64 matrix product
+    g = np.random.default_rng(7)
+    M, N, K = 48, 9, 160
+    w = oracle.f32_to_bf16(np.ldexp(g.integers(-8, 8, (M, K)), g.integers(-4, 2, (M, K)))
+                           .astype(np.float32))
+    x = oracle.f32_to_bf16(g.integers(-6, 7, (N, K)).astype(np.float32))
+    y = oracle.dense_gemm(w, x)
+    ref = oracle.bf16_to_f32(x).astype(np.float64) @ oracle.bf16_to_f32(w).astype(np.float64).T
+    assert np.array_equal(y, oracle.f32_to_bf16(ref.astype(np.float32)))
+
+
+def test_dense_gemm_one_hot_rows_and_zero_weights(oracle):
+    g = np.random.default_rng(8)
+    M, K = 32, 64
+    w = oracle.f32_to_bf16(g.standard_normal((M, K)).astype(np.float32))
+    x = np.zeros((3, K), np.uint16)
+    ks = [0, 17, 63]
+    for n, k in enumerate(ks):
+        x[n, k] = 0x3F80  # bf16 1.0
+    y = oracle.dense_gemm(w, x)
+    for n, k in enumerate(ks):  # a one-hot row returns that column of W, bit for bit
+        assert np.array_equal(y[n], w[:, k])
+    assert not oracle.dense_gemm(np.zeros_like(w), x).any()
+
+
+def test_dense_gemm_within_fp32_bound_of_fp64(oracle):
+    g = np.random.default_rng(9)
+    M, N, K = 64, 5, 512
+    w = oracle.f32_to_bf16((g.standard_normal((M, K)) * 0.02).astype(np.float32))
+    x = oracle.f32_to_bf16(g.standard_normal((N, K)).astype(np.float32))
+    wf = oracle.bf16_to_f32(w).astype(np.float64)
+    xf = oracle.bf16_to_f32(x).astype(np.float64)
+    exact = xf @ wf.T
+    got = oracle.bf16_to_f32(oracle.dense_gemm(w, x)).astype(np.float64)
+    # one bf16 rounding of the result plus K fp32 roundings of the running sum
+    bound = 2.0 ** -8 * np.abs(exact) + K * 2.0 ** -24 * (np.abs(xf) @ np.abs(wf).T)
+    assert (np.abs(got - exact) <= bound).all()
