@@ -195,6 +195,7 @@ def bench_c3(torch, args, results):
     log(f"C3: layer {ms * 1e3:.1f} us graph-replayed ({results['c3']['layer_gbs']:.0f} GB/s), "
         f"{eager_ms * 1e3:.1f} us eager; W13+SwiGLU {w13_ms * 1e3:.1f} us "
         f"({results['c3']['w13_gbs']:.0f} GB/s)")
+    bench_c3_shared(torch, args, results, moe, hidden, logits, bias)
     return dict(gate=gate, up=up, down=down, hidden=hidden_np, idx=idx,
                 w=tw.cpu().numpy(), bs=bs, alg_bytes=alg_bytes)
 
@@ -219,6 +220,52 @@ def cpu_baseline_c3(ctx, results):
                           kind="port", sample=f"{runs} full C3 layers (64 tokens, 48 experts)",
                           layer_ms=sec * 1e3)
     log(f"CPU baseline: {sec * 1e3:.0f} ms per layer on {threads} threads")
+
+
+def bench_c3_shared(torch, args, results, moe, normed, logits, bias):
+    """Beside the C3 routed layer: the Kimi shared expert (bf16 dense MLP, gate/up
+    [4096, 7168] and down [7168, 2048], seeded N(0, 0.02) weights) on the same 64
+    tokens, its gate/up GEMM alone, and the whole decode layer (shared expert,
+    router select, routed experts, residual join) as one HIP graph."""
+    import numpy as np
+    from pegainfer_amd import layer, synth
+    T, H, SI = 64, 7168, 2048
+    g = synth.rng(3, 4)
+    gu = dev(torch, synth.normal_bf16(g, (2 * SI, H), std=0.02), bf16=True)
+    dn = dev(torch, synth.normal_bf16(g, (H, SI), std=0.02), bf16=True)
+    shared = layer.KimiSharedExpert(gu, dn, max_tokens=T)
+    full = layer.KimiMoeDecodeLayer(moe, shared)
+    hidden = dev(torch, synth.normal_bf16(synth.rng(3, 5), (T, H)), bf16=True)
+    proj = torch.zeros(T, H, dtype=torch.bfloat16, device="cuda")
+    out = torch.zeros(T, H, dtype=torch.bfloat16, device="cuda")
+    from pegainfer_amd import ops
+    gemm_ms = time_graph(torch, lambda: ops.gemm_graphsafe(gu, normed, shared.gu[:T]),
+                         args.steps, args.warmup)
+    shared_ms = time_graph(torch, lambda: shared.forward(normed, proj), args.steps, args.warmup)
+    graph = layer.capture_graph(lambda: full.forward(hidden, normed, logits, bias, out))
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(torch.cuda.current_stream())
+    for _ in range(args.steps):
+        graph.replay()
+    e1.record(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    full_ms = e0.elapsed_time(e1) / args.steps
+    gemm_bytes = 2 * SI * H * 2 + T * H * 2 + T * 2 * SI * 2
+    shared_bytes = (2 * SI * H + H * SI) * 2 + T * H * 2 * 2
+    results["c3_shared"] = dict(
+        workload="c3_kimi_shared_expert_t64", tokens=T, hidden=H, inter=SI, launch="hip_graph",
+        gate_up_us=gemm_ms * 1e3, gate_up_bytes=gemm_bytes,
+        gate_up_gbs=gemm_bytes / (gemm_ms * 1e-3) / 1e9,
+        shared_us=shared_ms * 1e3, shared_bytes=shared_bytes,
+        shared_gbs=shared_bytes / (shared_ms * 1e-3) / 1e9,
+        full_layer_us=full_ms * 1e3)
+    log(f"C3 shared expert: gate/up GEMM {gemm_ms * 1e3:.1f} us "
+        f"({results['c3_shared']['gate_up_gbs']:.0f} GB/s), shared MLP {shared_ms * 1e3:.1f} us "
+        f"({results['c3_shared']['shared_gbs']:.0f} GB/s); full decode layer (shared + routed + "
+        f"join) {full_ms * 1e3:.1f} us graph-replayed")
 
 
 # ----------------------------------------------------------------------------- C1/C2

@@ -9,6 +9,13 @@
 // and called for the Kimi shared expert's gate/up and down projections
 // (pegainfer-kimi-k2/src/runner/moe_nccl.rs:107-123).
 //
+// Limit: the 16x16x32 fragment layout puts a different W (or X) row in each of
+// four neighbouring lanes, so every 16-byte-per-lane load splits into about 64
+// cache-line requests and the address unit, not HBM, bounds the kernel (78%
+// busy, ~77 cycles per load instruction on the Kimi gate/up shape; 1.6 TB/s of
+// W).  Reading 256 contiguous bytes per row per step instead (a permuted k
+// order) quadruples the lines per instruction and ran 2.3x slower.
+//
 // The decode-sized token counts this serves make the GEMM a weight stream, so
 // one workgroup owns 16 output features for up to 64 tokens and reads its W
 // rows from HBM exactly once; its WK waves split K and are reduced through
@@ -30,8 +37,11 @@ typedef __attribute__((__vector_size__(4 * sizeof(float)))) float floatx4_t;
 typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4_t;
 
 constexpr uint32_t kOutOfRange = 0x80000000u;  // voffset that fails every range check
+// W loads are cached too: a step reads 64 bytes of each of 16 rows, so the
+// other half of every 128-byte line is the next step's, and a non-temporal
+// policy that does not keep the line costs 20% (44.9 against 37.3 us for
+// the Kimi gate/up shape).
 constexpr int kCached = 0;
-constexpr int kStream = 2;  // non-temporal: W is read exactly once per launch
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
@@ -82,7 +92,7 @@ __global__ __launch_bounds__(64 * WK) void dense_gemm_kernel(const uint16_t* __r
   auto load_step = [&](StepRegs<RB>& r, int s) {
     s = min(max(s, 0), steps - 1);  // every scalar offset stays inside the rows
     const uint32_t soff = static_cast<uint32_t>(s) * 64u;
-    r.w = load16<kStream>(wr, w_voff, soff);
+    r.w = load16<kCached>(wr, w_voff, soff);
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) r.x[rb] = load16<kCached>(xr, x_voff[rb], soff);
   };
