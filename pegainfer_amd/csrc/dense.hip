@@ -9,20 +9,24 @@
 // and called for the Kimi shared expert's gate/up and down projections
 // (pegainfer-kimi-k2/src/runner/moe_nccl.rs:107-123).
 //
-// Limit: the 16x16x32 fragment layout puts a different W (or X) row in each of
-// four neighbouring lanes, so every 16-byte-per-lane load splits into about 64
-// cache-line requests and the address unit, not HBM, bounds the kernel (78%
-// busy, ~77 cycles per load instruction on the Kimi gate/up shape; 1.6 TB/s of
-// W).  Reading 256 contiguous bytes per row per step instead (a permuted k
-// order) quadruples the lines per instruction and ran 2.3x slower.
+// Load shape: the 16x16x32 fragment layout puts a different W (or X) row in
+// each of four neighbouring lanes; loaded that way, every 16-byte-per-lane
+// load splits into about 64 cache-line requests and the address unit bounds
+// the kernel (78% busy, ~77 cycles per load instruction, 1.6 TB/s of W on the
+// Kimi gate/up shape).  So the loads run along k (a lane quad reads 64
+// contiguous bytes of one row) and ds_bpermute moves each lane's 16 bytes to
+// the lane whose fragment needs them: gate/up 37.3 -> 26.4 us (2.3 TB/s of W).
+// A permuted k order that reads 256 contiguous bytes per row per step instead
+// quadruples the lines per instruction and ran 2.3x slower.
 //
 // The decode-sized token counts this serves make the GEMM a weight stream, so
 // one workgroup owns 16 output features for up to 64 tokens and reads its W
 // rows from HBM exactly once; its WK waves split K and are reduced through
 // LDS in wave order (deterministic).  Per 32-k step a lane issues one 16-byte
-// load of W (row m0 + c, k 8q..8q+7: the B fragment of a 16x16x32 MFMA, no
-// transpose) and one 16-byte load of X per 16-token row block (the A
-// fragment), then one v_mfma_f32_16x16x32_bf16 per row block.  A and B take
+// load of W and one of X per 16-token row block; after the lane exchange,
+// lane (c, q) holds row m0 + c, k 8q..8q+7 (the B fragment of a 16x16x32
+// MFMA) and the row blocks' A fragments, and one v_mfma_f32_16x16x32_bf16
+// runs per row block.  A and B take
 // the same k slots per lane, so the product is exact whatever k order the
 // MFMA assigns to them.  Token rows past N read zeros through an
 // out-of-range buffer offset and are never stored.
@@ -56,8 +60,8 @@ __device__ __forceinline__ u32x4_t load16(__amdgpu_buffer_rsrc_t r, uint32_t vof
 
 template <int RB>
 struct StepRegs {
-  u32x4_t w;      // B fragment: W[m0 + c][k0 + 8q .. +7]
-  u32x4_t x[RB];  // A fragments: X[n0 + 16 rb + c][k0 + 8q .. +7]
+  u32x4_t w;      // W[m0 + l / 4][k0 + 8 (l % 4) .. +7] (lane l)
+  u32x4_t x[RB];  // X[n0 + 16 rb + l / 4][k0 + 8 (l % 4) .. +7]
 };
 
 // One workgroup per (16 output features, 16 RB tokens); WK waves split the
@@ -79,15 +83,29 @@ __global__ __launch_bounds__(64 * WK) void dense_gemm_kernel(const uint16_t* __r
 
   const __amdgpu_buffer_rsrc_t wr =
       make_rsrc(W + static_cast<long long>(m0) * K, 16u * static_cast<uint32_t>(K) * 2u);
-  const uint32_t w_voff = (static_cast<uint32_t>(c) * K + 8u * q) * 2u;
+  // Loads run along k: lane l fetches row l / 4, k 8 (l % 4) .. +7, so four
+  // neighbouring lanes read 64 contiguous bytes of one row (one line request
+  // per lane quad, 16 per load); ds_bpermute then hands lane (c, q) the
+  // 16 bytes of row c, k 8q .. +7 that its fragment needs, from lane 4c + q.
+  const uint32_t lr = static_cast<uint32_t>(lane >> 2), lp = static_cast<uint32_t>(lane & 3);
+  const uint32_t w_voff = (lr * K + 8u * lp) * 2u;
+  const int src_lane_bytes = (4 * c + q) * 4;
   const __amdgpu_buffer_rsrc_t xr =
       make_rsrc(X, static_cast<uint32_t>(N) * static_cast<uint32_t>(K) * 2u);
   uint32_t x_voff[RB];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
-    const int n = n0 + 16 * rb + c;
-    x_voff[rb] = n < N ? (static_cast<uint32_t>(n) * K + 8u * q) * 2u : kOutOfRange;
+    const int n = n0 + 16 * rb + static_cast<int>(lr);
+    x_voff[rb] = n < N ? (static_cast<uint32_t>(n) * K + 8u * lp) * 2u : kOutOfRange;
   }
+  auto to_fragment = [&](u32x4_t v) {
+    u32x4_t f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      f[e] = static_cast<uint32_t>(
+          __builtin_amdgcn_ds_bpermute(src_lane_bytes, static_cast<int>(v[e])));
+    return f;
+  };
 
   auto load_step = [&](StepRegs<RB>& r, int s) {
     s = min(max(s, 0), steps - 1);  // every scalar offset stays inside the rows
@@ -100,11 +118,11 @@ __global__ __launch_bounds__(64 * WK) void dense_gemm_kernel(const uint16_t* __r
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) acc[rb] = floatx4_t{};
   auto compute_step = [&](const StepRegs<RB>& r) {
-    const bf16x8_t b = __builtin_bit_cast(bf16x8_t, r.w);
+    const bf16x8_t b = __builtin_bit_cast(bf16x8_t, to_fragment(r.w));
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
-      acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, r.x[rb]), b,
-                                                         acc[rb], 0, 0, 0);
+      acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+          __builtin_bit_cast(bf16x8_t, to_fragment(r.x[rb])), b, acc[rb], 0, 0, 0);
   };
 
   StepRegs<RB> slot[D];
