@@ -19,14 +19,14 @@
 // A permuted k order that reads 256 contiguous bytes per row per step instead
 // quadruples the lines per instruction and ran 2.3x slower.
 //
-// The decode-sized token counts this serves make the GEMM a weight stream, so
-// one workgroup owns 16 output features for up to 64 tokens and reads its W
-// rows from HBM exactly once; its WK waves split K and are reduced through
-// LDS in wave order (deterministic).  Per 32-k step a lane issues one 16-byte
-// load of W and one of X per 16-token row block; after the lane exchange,
-// lane (c, q) holds row m0 + c, k 8q..8q+7 (the B fragment of a 16x16x32
-// MFMA) and the row blocks' A fragments, and one v_mfma_f32_16x16x32_bf16
-// runs per row block.  A and B take
+// The decode-sized token counts this serves make the GEMM a weight stream:
+// one workgroup owns 16 MR output features for 16 RB tokens (the host picks
+// the shape); its WK waves split K and are reduced through LDS in wave order
+// (deterministic).  Per 32-k step a lane issues one 16-byte load of W per
+// 16-feature row tile and one of X per 16-token row block; after the lane
+// exchange, lane (c, q) holds feature m0 + 16 mr + c, k 8q..8q+7 (the B
+// fragment of a 16x16x32 MFMA) and the token blocks' A fragments, and one
+// v_mfma_f32_16x16x32_bf16 runs per (row tile, token block).  A and B take
 // the same k slots per lane, so the product is exact whatever k order the
 // MFMA assigns to them.  Token rows past N read zeros through an
 // out-of-range buffer offset and are never stored.
@@ -58,37 +58,40 @@ __device__ __forceinline__ u32x4_t load16(__amdgpu_buffer_rsrc_t r, uint32_t vof
                                                kPolicy);
 }
 
-template <int RB>
+template <int MR, int RB>
 struct StepRegs {
-  u32x4_t w;      // W[m0 + l / 4][k0 + 8 (l % 4) .. +7] (lane l)
+  u32x4_t w[MR];  // W[m0 + 16 mr + l / 4][k0 + 8 (l % 4) .. +7] (lane l)
   u32x4_t x[RB];  // X[n0 + 16 rb + l / 4][k0 + 8 (l % 4) .. +7]
 };
 
-// One workgroup per (16 output features, 16 RB tokens); WK waves split the
-// K/32 steps; D steps per wave in flight.
-template <int WK, int RB>
+// One workgroup per (16 MR output features, 16 RB tokens); WK waves split the
+// K/32 steps; D steps per wave in flight.  Each X fragment feeds MR MFMAs and
+// each W fragment RB.
+template <int WK, int MR, int RB>
 __global__ __launch_bounds__(64 * WK) void dense_gemm_kernel(const uint16_t* __restrict__ W,
                                                              const uint16_t* __restrict__ X,
                                                              uint16_t* __restrict__ Y, int M,
                                                              int N, int K) {
-  constexpr int D = 4;
+  constexpr int D = MR + RB <= 5 ? 4 : 3;  // the ring fits 128 VGPRs at WK = 16
   __shared__ float s_red[WK][RB * 4][64];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c = lane & 15, q = lane >> 4;
-  const int m0 = blockIdx.x * 16;
+  const int m0 = blockIdx.x * 16 * MR;
   const int n0 = blockIdx.y * (16 * RB);
   const int steps = K >> 5;
   const int s0 = (steps * wave) / WK, s1 = (steps * (wave + 1)) / WK;
 
-  const __amdgpu_buffer_rsrc_t wr =
-      make_rsrc(W + static_cast<long long>(m0) * K, 16u * static_cast<uint32_t>(K) * 2u);
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(
+      W + static_cast<long long>(m0) * K, 16u * MR * static_cast<uint32_t>(K) * 2u);
   // Loads run along k: lane l fetches row l / 4, k 8 (l % 4) .. +7, so four
   // neighbouring lanes read 64 contiguous bytes of one row (one line request
   // per lane quad, 16 per load); ds_bpermute then hands lane (c, q) the
   // 16 bytes of row c, k 8q .. +7 that its fragment needs, from lane 4c + q.
   const uint32_t lr = static_cast<uint32_t>(lane >> 2), lp = static_cast<uint32_t>(lane & 3);
-  const uint32_t w_voff = (lr * K + 8u * lp) * 2u;
+  uint32_t w_voff[MR];
+#pragma unroll
+  for (int mr = 0; mr < MR; ++mr) w_voff[mr] = ((16u * mr + lr) * K + 8u * lp) * 2u;
   const int src_lane_bytes = (4 * c + q) * 4;
   const __amdgpu_buffer_rsrc_t xr =
       make_rsrc(X, static_cast<uint32_t>(N) * static_cast<uint32_t>(K) * 2u);
@@ -104,28 +107,36 @@ __global__ __launch_bounds__(64 * WK) void dense_gemm_kernel(const uint16_t* __r
     for (int e = 0; e < 4; ++e)
       f[e] = static_cast<uint32_t>(
           __builtin_amdgcn_ds_bpermute(src_lane_bytes, static_cast<int>(v[e])));
-    return f;
+    return __builtin_bit_cast(bf16x8_t, f);
   };
 
-  auto load_step = [&](StepRegs<RB>& r, int s) {
+  auto load_step = [&](StepRegs<MR, RB>& r, int s) {
     s = min(max(s, 0), steps - 1);  // every scalar offset stays inside the rows
     const uint32_t soff = static_cast<uint32_t>(s) * 64u;
-    r.w = load16<kCached>(wr, w_voff, soff);
+#pragma unroll
+    for (int mr = 0; mr < MR; ++mr) r.w[mr] = load16<kCached>(wr, w_voff[mr], soff);
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) r.x[rb] = load16<kCached>(xr, x_voff[rb], soff);
   };
-  floatx4_t acc[RB];
+  floatx4_t acc[MR][RB];
 #pragma unroll
-  for (int rb = 0; rb < RB; ++rb) acc[rb] = floatx4_t{};
-  auto compute_step = [&](const StepRegs<RB>& r) {
-    const bf16x8_t b = __builtin_bit_cast(bf16x8_t, to_fragment(r.w));
+  for (int mr = 0; mr < MR; ++mr)
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb)
-      acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-          __builtin_bit_cast(bf16x8_t, to_fragment(r.x[rb])), b, acc[rb], 0, 0, 0);
+    for (int rb = 0; rb < RB; ++rb) acc[mr][rb] = floatx4_t{};
+  auto compute_step = [&](const StepRegs<MR, RB>& r) {
+    bf16x8_t a[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) a[rb] = to_fragment(r.x[rb]);
+#pragma unroll
+    for (int mr = 0; mr < MR; ++mr) {
+      const bf16x8_t b = to_fragment(r.w[mr]);
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+        acc[mr][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[rb], b, acc[mr][rb], 0, 0, 0);
+    }
   };
 
-  StepRegs<RB> slot[D];
+  StepRegs<MR, RB> slot[D];
 #pragma unroll
   for (int j = 0; j < D; ++j) {
     load_step(slot[j], s0 + j < s1 ? s0 + j : s1 - 1);
@@ -148,32 +159,66 @@ __global__ __launch_bounds__(64 * WK) void dense_gemm_kernel(const uint16_t* __r
   for (int j = 0; j < D - 1; ++j)
     if (s + j < s1) compute_step(slot[j]);
 
-  // Reduction over the WK waves in wave order.  Accumulator element e of row
-  // block rb holds token n0 + 16 rb + 4 q + e, feature m0 + c.
+  // Reduction over the WK waves in wave order, one row tile at a time.
+  // Accumulator element e of (mr, rb) holds token n0 + 16 rb + 4 q + e,
+  // feature m0 + 16 mr + c.
 #pragma unroll
-  for (int rb = 0; rb < RB; ++rb)
+  for (int mr = 0; mr < MR; ++mr) {
+    if (mr > 0) __syncthreads();  // the previous tile's sums are read
 #pragma unroll
-    for (int e = 0; e < 4; ++e) s_red[wave][rb * 4 + e][lane] = acc[rb][e];
-  __syncthreads();
-  for (int j = wave; j < RB * 4; j += WK) {
-    float sum = 0.0f;
+    for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-    for (int w = 0; w < WK; ++w) sum += s_red[w][j][lane];
-    const int n = n0 + 16 * (j >> 2) + 4 * q + (j & 3);
-    if (n < N) Y[static_cast<long long>(n) * M + m0 + c] = f2bf(sum);
+      for (int e = 0; e < 4; ++e) s_red[wave][rb * 4 + e][lane] = acc[mr][rb][e];
+    __syncthreads();
+    for (int j = wave; j < RB * 4; j += WK) {
+      float sum = 0.0f;
+#pragma unroll
+      for (int w = 0; w < WK; ++w) sum += s_red[w][j][lane];
+      const int n = n0 + 16 * (j >> 2) + 4 * q + (j & 3);
+      if (n < N) Y[static_cast<long long>(n) * M + m0 + 16 * mr + c] = f2bf(sum);
+    }
+  }
+}
+
+template <int WK, int MR>
+void launch_dense_rb(int rb, dim3 grid, const uint16_t* W, const uint16_t* X, uint16_t* Y, int M,
+                     int N, int K, hipStream_t stream) {
+  const dim3 block(64 * WK);
+  switch (rb) {
+    case 1: hipLaunchKernelGGL((dense_gemm_kernel<WK, MR, 1>), grid, block, 0, stream, W, X, Y, M, N, K); break;
+    case 2: hipLaunchKernelGGL((dense_gemm_kernel<WK, MR, 2>), grid, block, 0, stream, W, X, Y, M, N, K); break;
+    case 3: hipLaunchKernelGGL((dense_gemm_kernel<WK, MR, 3>), grid, block, 0, stream, W, X, Y, M, N, K); break;
+    default: hipLaunchKernelGGL((dense_gemm_kernel<WK, MR, 4>), grid, block, 0, stream, W, X, Y, M, N, K); break;
   }
 }
 
 template <int WK>
-void launch_dense(int rb, dim3 grid, const uint16_t* W, const uint16_t* X, uint16_t* Y, int M,
-                  int N, int K, hipStream_t stream) {
-  const dim3 block(64 * WK);
-  switch (rb) {
-    case 1: hipLaunchKernelGGL((dense_gemm_kernel<WK, 1>), grid, block, 0, stream, W, X, Y, M, N, K); break;
-    case 2: hipLaunchKernelGGL((dense_gemm_kernel<WK, 2>), grid, block, 0, stream, W, X, Y, M, N, K); break;
-    case 3: hipLaunchKernelGGL((dense_gemm_kernel<WK, 3>), grid, block, 0, stream, W, X, Y, M, N, K); break;
-    default: hipLaunchKernelGGL((dense_gemm_kernel<WK, 4>), grid, block, 0, stream, W, X, Y, M, N, K); break;
+void launch_dense(int mr, int rb, dim3 grid, const uint16_t* W, const uint16_t* X, uint16_t* Y,
+                  int M, int N, int K, hipStream_t stream) {
+  switch (mr) {
+    case 2: launch_dense_rb<WK, 2>(rb, grid, W, X, Y, M, N, K, stream); break;
+    default: launch_dense_rb<WK, 1>(rb, grid, W, X, Y, M, N, K, stream); break;
   }
+}
+
+// Row tiles per wave: two where M allows (each X fragment then feeds two
+// MFMAs).  Token blocks per workgroup: up to four, halved once when the grid
+// would leave CUs idle.  Filling the CUs is worth more than reading each W row
+// once: the workgroups that share W rows sit at the same blockIdx.x, and since
+// M / 32 is a multiple of 8 on the shapes this serves (4096, 7168) they land on
+// the same XCD and find the rows in its L2 (Kimi gate/up, 64 tokens:
+// 128 workgroups of 64 tokens 26.4 us, 256 of 32 tokens 20.4 us).
+struct DenseShape {
+  int mr, rb;
+};
+
+DenseShape pick_shape(int M, int N, int cu) {
+  DenseShape d;
+  d.mr = M % 32 == 0 ? 2 : 1;
+  d.rb = N <= 16 ? 1 : N <= 32 ? 2 : N <= 48 ? 3 : 4;
+  const long long gx = M / (16 * d.mr);
+  if (d.rb > 1 && gx * ceil_div(N, 16 * d.rb) < cu) d.rb = (d.rb + 1) / 2;
+  return d;
 }
 
 int dense_gemm(const uint16_t* W, const uint16_t* X, uint16_t* Y, int M, int N, int K,
@@ -191,19 +236,21 @@ int dense_gemm(const uint16_t* W, const uint16_t* X, uint16_t* Y, int M, int N, 
     return fail(kNotSupported, "%s: X over 2 GiB (N=%d K=%d)", name, N, K);
   const int cu = current_cu_count();
   if (cu <= 0) return fail(kInvalidValue, "%s: no device", name);
-  const int rb = N <= 16 ? 1 : N <= 32 ? 2 : N <= 48 ? 3 : 4;
-  const dim3 grid(M / 16, ceil_div(N, 16 * rb));
-  if (grid.y > 65535u) return fail(kNotSupported, "%s: too many token blocks (N=%d)", name, N);
+  const DenseShape shape = pick_shape(M, N, cu);
+  const int mr = shape.mr, rb = shape.rb;
+  const int ny = ceil_div(N, 16 * rb);
+  if (ny > 65535) return fail(kNotSupported, "%s: too many token blocks (N=%d)", name, N);
+  const dim3 grid(M / (16 * mr), ny);
   // Few workgroups: more waves each, splitting K (at least one step a wave).
   const long long wgs = static_cast<long long>(grid.x) * grid.y;
   int wk = wgs <= cu ? 16 : (wgs <= 2LL * cu ? 8 : 4);
   while (wk > 1 && K / 32 < wk) wk >>= 1;
   switch (wk) {
-    case 16: launch_dense<16>(rb, grid, W, X, Y, M, N, K, stream); break;
-    case 8: launch_dense<8>(rb, grid, W, X, Y, M, N, K, stream); break;
-    case 4: launch_dense<4>(rb, grid, W, X, Y, M, N, K, stream); break;
-    case 2: launch_dense<2>(rb, grid, W, X, Y, M, N, K, stream); break;
-    default: launch_dense<1>(rb, grid, W, X, Y, M, N, K, stream); break;
+    case 16: launch_dense<16>(mr, rb, grid, W, X, Y, M, N, K, stream); break;
+    case 8: launch_dense<8>(mr, rb, grid, W, X, Y, M, N, K, stream); break;
+    case 4: launch_dense<4>(mr, rb, grid, W, X, Y, M, N, K, stream); break;
+    case 2: launch_dense<2>(mr, rb, grid, W, X, Y, M, N, K, stream); break;
+    default: launch_dense<1>(mr, rb, grid, W, X, Y, M, N, K, stream); break;
   }
   return launch_status(name);
 }
