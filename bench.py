@@ -225,7 +225,7 @@ def cpu_baseline_c3(ctx, results):
 def bench_c3_shared(torch, args, results, moe, normed, logits, bias):
     """Beside the C3 routed layer: the Kimi shared expert (bf16 dense MLP, gate/up
     [4096, 7168] and down [7168, 2048], seeded N(0, 0.02) weights) on the same 64
-    tokens, its gate/up GEMM alone, and the whole decode layer (shared expert,
+    tokens, its gate/up GEMM with the SwiGLU epilogue alone, and the whole decode layer (shared expert,
     router select, routed experts, residual join) as one HIP graph."""
     import numpy as np
     from pegainfer_amd import layer, synth
@@ -239,7 +239,7 @@ def bench_c3_shared(torch, args, results, moe, normed, logits, bias):
     proj = torch.zeros(T, H, dtype=torch.bfloat16, device="cuda")
     out = torch.zeros(T, H, dtype=torch.bfloat16, device="cuda")
     from pegainfer_amd import ops
-    gemm_ms = time_graph(torch, lambda: ops.gemm_graphsafe(gu, normed, shared.gu[:T]),
+    gemm_ms = time_graph(torch, lambda: ops.dense_w13_swiglu(gu, normed, shared.act[:T]),
                          args.steps, args.warmup)
     shared_ms = time_graph(torch, lambda: shared.forward(normed, proj), args.steps, args.warmup)
     graph = layer.capture_graph(lambda: full.forward(hidden, normed, logits, bias, out))
@@ -253,7 +253,7 @@ def bench_c3_shared(torch, args, results, moe, normed, logits, bias):
     e1.record(torch.cuda.current_stream())
     torch.cuda.synchronize()
     full_ms = e0.elapsed_time(e1) / args.steps
-    gemm_bytes = 2 * SI * H * 2 + T * H * 2 + T * 2 * SI * 2
+    gemm_bytes = 2 * SI * H * 2 + T * H * 2 + T * SI * 2
     shared_bytes = (2 * SI * H + H * SI) * 2 + T * H * 2 * 2
     results["c3_shared"] = dict(
         workload="c3_kimi_shared_expert_t64", tokens=T, hidden=H, inter=SI, launch="hip_graph",
@@ -262,7 +262,7 @@ def bench_c3_shared(torch, args, results, moe, normed, logits, bias):
         shared_us=shared_ms * 1e3, shared_bytes=shared_bytes,
         shared_gbs=shared_bytes / (shared_ms * 1e-3) / 1e9,
         full_layer_us=full_ms * 1e3)
-    log(f"C3 shared expert: gate/up GEMM {gemm_ms * 1e3:.1f} us "
+    log(f"C3 shared expert: gate/up GEMM + SwiGLU {gemm_ms * 1e3:.1f} us "
         f"({results['c3_shared']['gate_up_gbs']:.0f} GB/s), shared MLP {shared_ms * 1e3:.1f} us "
         f"({results['c3_shared']['shared_gbs']:.0f} GB/s); full decode layer (shared + routed + "
         f"join) {full_ms * 1e3:.1f} us graph-replayed")

@@ -240,6 +240,15 @@ int gemm_cuda(const uint16_t* W, const uint16_t* X, uint16_t* Y, int M, int N, i
 int gemm_graphsafe_cuda(const uint16_t* W, const uint16_t* X, uint16_t* Y, int M, int N, int K,
                         hipStream_t stream);
 
+/* No reference symbol of its own: gemm_graphsafe_cuda on the shared expert's gate/up weights
+ * W13 [2 inter][K] (gate rows first) followed by kimi_marlin_w13_swiglu_cuda on its bf16 output,
+ * as pegainfer-kimi-k2/src/runner/moe_nccl.rs:107-123 runs them, in one launch with the same
+ * bits: act[n][j] = SwiGLU(bf16 gate sum, bf16 up sum).  X [N][K], act [N][inter].  Needs
+ * inter % 16 == 0, K % 32 == 0 and 16-byte aligned W13 and X (801 otherwise).  Never
+ * allocates. */
+int pega_dense_w13_swiglu(const uint16_t* W13, const uint16_t* X, uint16_t* act, int inter, int N,
+                          int K, hipStream_t stream);
+
 /* ---------------- routing select ---------------- */
 
 /* No reference symbol of its own: the select stage (sigmoid, top-k of score+bias, renormalise)

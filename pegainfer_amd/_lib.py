@@ -59,6 +59,7 @@ SIGNATURES = {
     "pega_wna16_prefill_pair": [ctypes.POINTER(Wna16Problem), ctypes.POINTER(Wna16Problem), _P],
     "gemm_cuda": [_P, _P, _P, _I, _I, _I, _P],
     "gemm_graphsafe_cuda": [_P, _P, _P, _I, _I, _I, _P],
+    "pega_dense_w13_swiglu": [_P, _P, _P, _I, _I, _I, _P],
 }
 _RESTYPE = {"pegainfer_kernels_last_error": ctypes.c_char_p}
 

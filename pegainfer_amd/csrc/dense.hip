@@ -66,24 +66,30 @@ struct StepRegs {
 
 // One workgroup per (16 MR output features, 16 RB tokens); WK waves split the
 // K/32 steps; D steps per wave in flight.  Each X fragment feeds MR MFMAs and
-// each W fragment RB.
-template <int WK, int MR, int RB>
+// each W fragment RB.  A wave's row tiles start tile_stride rows apart.
+// SWIGLU (MR = 2): tile 0 holds gate features m0..m0+15 and tile 1 the
+// matching up features (tile_stride = I); the epilogue rounds both sums to
+// bf16 as the GEMM's output would be, applies SwiGLU and writes act[n][m0+c]
+// (Y row stride M = I).
+template <int WK, int MR, int RB, bool SWIGLU>
 __global__ __launch_bounds__(64 * WK) void dense_gemm_kernel(const uint16_t* __restrict__ W,
                                                              const uint16_t* __restrict__ X,
                                                              uint16_t* __restrict__ Y, int M,
-                                                             int N, int K) {
+                                                             int N, int K, int tile_stride) {
+  static_assert(!SWIGLU || MR == 2, "SwiGLU pairs one gate and one up tile");
   constexpr int D = MR + RB <= 5 ? 4 : 3;  // the ring fits 128 VGPRs at WK = 16
   __shared__ float s_red[WK][RB * 4][64];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c = lane & 15, q = lane >> 4;
-  const int m0 = blockIdx.x * 16 * MR;
+  const int m0 = blockIdx.x * (SWIGLU ? 16 : 16 * MR);
   const int n0 = blockIdx.y * (16 * RB);
   const int steps = K >> 5;
   const int s0 = (steps * wave) / WK, s1 = (steps * (wave + 1)) / WK;
 
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(
-      W + static_cast<long long>(m0) * K, 16u * MR * static_cast<uint32_t>(K) * 2u);
+      W + static_cast<long long>(m0) * K,
+      (static_cast<uint32_t>(tile_stride) * (MR - 1) + 16u) * static_cast<uint32_t>(K) * 2u);
   // Loads run along k: lane l fetches row l / 4, k 8 (l % 4) .. +7, so four
   // neighbouring lanes read 64 contiguous bytes of one row (one line request
   // per lane quad, 16 per load); ds_bpermute then hands lane (c, q) the
@@ -91,7 +97,7 @@ __global__ __launch_bounds__(64 * WK) void dense_gemm_kernel(const uint16_t* __r
   const uint32_t lr = static_cast<uint32_t>(lane >> 2), lp = static_cast<uint32_t>(lane & 3);
   uint32_t w_voff[MR];
 #pragma unroll
-  for (int mr = 0; mr < MR; ++mr) w_voff[mr] = ((16u * mr + lr) * K + 8u * lp) * 2u;
+  for (int mr = 0; mr < MR; ++mr) w_voff[mr] = ((static_cast<uint32_t>(tile_stride) * mr + lr) * K + 8u * lp) * 2u;
   const int src_lane_bytes = (4 * c + q) * 4;
   const __amdgpu_buffer_rsrc_t xr =
       make_rsrc(X, static_cast<uint32_t>(N) * static_cast<uint32_t>(K) * 2u);
@@ -161,7 +167,10 @@ __global__ __launch_bounds__(64 * WK) void dense_gemm_kernel(const uint16_t* __r
 
   // Reduction over the WK waves in wave order, one row tile at a time.
   // Accumulator element e of (mr, rb) holds token n0 + 16 rb + 4 q + e,
-  // feature m0 + 16 mr + c.
+  // feature m0 + tile_stride mr + c.  Every tile gives a lane the same j
+  // values, so a SwiGLU lane keeps its gate sums in gsum for the up pass.
+  constexpr int kJ = (RB * 4 + WK - 1) / WK;
+  float gsum[kJ];
 #pragma unroll
   for (int mr = 0; mr < MR; ++mr) {
     if (mr > 0) __syncthreads();  // the previous tile's sums are read
@@ -170,59 +179,68 @@ __global__ __launch_bounds__(64 * WK) void dense_gemm_kernel(const uint16_t* __r
 #pragma unroll
       for (int e = 0; e < 4; ++e) s_red[wave][rb * 4 + e][lane] = acc[mr][rb][e];
     __syncthreads();
-    for (int j = wave; j < RB * 4; j += WK) {
+#pragma unroll
+    for (int i = 0; i < kJ; ++i) {
+      const int j = wave + i * WK;
+      if (j >= RB * 4) break;
       float sum = 0.0f;
 #pragma unroll
       for (int w = 0; w < WK; ++w) sum += s_red[w][j][lane];
       const int n = n0 + 16 * (j >> 2) + 4 * q + (j & 3);
-      if (n < N) Y[static_cast<long long>(n) * M + m0 + 16 * mr + c] = f2bf(sum);
+      if constexpr (SWIGLU) {
+        if (mr == 0) {
+          gsum[i] = sum;
+        } else if (n < N) {
+          Y[static_cast<long long>(n) * M + m0 + c] =
+              swiglu_one(bf2f(f2bf(gsum[i])), bf2f(f2bf(sum)));
+        }
+      } else if (n < N) {
+        Y[static_cast<long long>(n) * M + m0 + 16 * mr + c] = f2bf(sum);
+      }
     }
   }
 }
 
-template <int WK, int MR>
+template <int WK, int MR, bool SWIGLU>
 void launch_dense_rb(int rb, dim3 grid, const uint16_t* W, const uint16_t* X, uint16_t* Y, int M,
-                     int N, int K, hipStream_t stream) {
+                     int N, int K, int stride, hipStream_t stream) {
   const dim3 block(64 * WK);
   switch (rb) {
-    case 1: hipLaunchKernelGGL((dense_gemm_kernel<WK, MR, 1>), grid, block, 0, stream, W, X, Y, M, N, K); break;
-    case 2: hipLaunchKernelGGL((dense_gemm_kernel<WK, MR, 2>), grid, block, 0, stream, W, X, Y, M, N, K); break;
-    case 3: hipLaunchKernelGGL((dense_gemm_kernel<WK, MR, 3>), grid, block, 0, stream, W, X, Y, M, N, K); break;
-    default: hipLaunchKernelGGL((dense_gemm_kernel<WK, MR, 4>), grid, block, 0, stream, W, X, Y, M, N, K); break;
+    case 1: hipLaunchKernelGGL((dense_gemm_kernel<WK, MR, 1, SWIGLU>), grid, block, 0, stream, W, X, Y, M, N, K, stride); break;
+    case 2: hipLaunchKernelGGL((dense_gemm_kernel<WK, MR, 2, SWIGLU>), grid, block, 0, stream, W, X, Y, M, N, K, stride); break;
+    case 3: hipLaunchKernelGGL((dense_gemm_kernel<WK, MR, 3, SWIGLU>), grid, block, 0, stream, W, X, Y, M, N, K, stride); break;
+    default: hipLaunchKernelGGL((dense_gemm_kernel<WK, MR, 4, SWIGLU>), grid, block, 0, stream, W, X, Y, M, N, K, stride); break;
   }
 }
 
-template <int WK>
+template <int WK, bool SWIGLU>
 void launch_dense(int mr, int rb, dim3 grid, const uint16_t* W, const uint16_t* X, uint16_t* Y,
-                  int M, int N, int K, hipStream_t stream) {
-  switch (mr) {
-    case 2: launch_dense_rb<WK, 2>(rb, grid, W, X, Y, M, N, K, stream); break;
-    default: launch_dense_rb<WK, 1>(rb, grid, W, X, Y, M, N, K, stream); break;
-  }
+                  int M, int N, int K, int stride, hipStream_t stream) {
+  if (SWIGLU || mr == 2)
+    launch_dense_rb<WK, 2, SWIGLU>(rb, grid, W, X, Y, M, N, K, stride, stream);
+  else
+    launch_dense_rb<WK, 1, false>(rb, grid, W, X, Y, M, N, K, stride, stream);
 }
 
 // Row tiles per wave: two where M allows (each X fragment then feeds two
 // MFMAs).  Token blocks per workgroup: up to four, halved once when the grid
 // would leave CUs idle.  Filling the CUs is worth more than reading each W row
 // once: the workgroups that share W rows sit at the same blockIdx.x, and since
-// M / 32 is a multiple of 8 on the shapes this serves (4096, 7168) they land on
-// the same XCD and find the rows in its L2 (Kimi gate/up, 64 tokens:
-// 128 workgroups of 64 tokens 26.4 us, 256 of 32 tokens 20.4 us).
-struct DenseShape {
-  int mr, rb;
-};
-
-DenseShape pick_shape(int M, int N, int cu) {
-  DenseShape d;
-  d.mr = M % 32 == 0 ? 2 : 1;
-  d.rb = N <= 16 ? 1 : N <= 32 ? 2 : N <= 48 ? 3 : 4;
-  const long long gx = M / (16 * d.mr);
-  if (d.rb > 1 && gx * ceil_div(N, 16 * d.rb) < cu) d.rb = (d.rb + 1) / 2;
-  return d;
+// the row-tile count is a multiple of 8 on the shapes this serves (4096, 7168
+// features) they land on the same XCD and find the rows in its L2 (Kimi
+// gate/up, 64 tokens: 128 workgroups of 64 tokens 26.4 us, 256 of 32 tokens
+// 20.4 us).
+int pick_token_blocks(long long row_groups, int N, int cu) {
+  int rb = N <= 16 ? 1 : N <= 32 ? 2 : N <= 48 ? 3 : 4;
+  if (rb > 1 && row_groups * ceil_div(N, 16 * rb) < cu) rb = (rb + 1) / 2;
+  return rb;
 }
 
-int dense_gemm(const uint16_t* W, const uint16_t* X, uint16_t* Y, int M, int N, int K,
-               hipStream_t stream, const char* name) {
+// Shared checks and launch.  rows = W rows read (M, or 2 I for SwiGLU),
+// M = output features per token row of Y.
+template <bool SWIGLU>
+int dense_launch(const uint16_t* W, const uint16_t* X, uint16_t* Y, int rows, int M, int N, int K,
+                 hipStream_t stream, const char* name) {
   if (!W || !X || !Y) return fail(kInvalidValue, "%s: null pointer", name);
   if (M <= 0 || N <= 0 || K <= 0)
     return fail(kInvalidValue, "%s: bad shape M=%d N=%d K=%d", name, M, N, K);
@@ -230,27 +248,30 @@ int dense_gemm(const uint16_t* W, const uint16_t* X, uint16_t* Y, int M, int N, 
     return fail(kNotSupported, "%s: M %% 16 and K %% 32 must be 0 (M=%d K=%d)", name, M, K);
   if ((reinterpret_cast<uintptr_t>(W) & 15u) != 0 || (reinterpret_cast<uintptr_t>(X) & 15u) != 0)
     return fail(kInvalidValue, "%s: W and X must be 16-byte aligned", name);
-  // X is addressed through one 32-bit buffer range that must stay below the
-  // out-of-range offset
-  if (static_cast<long long>(N) * K * 2 >= static_cast<long long>(kOutOfRange))
-    return fail(kNotSupported, "%s: X over 2 GiB (N=%d K=%d)", name, N, K);
+  // X (and a SwiGLU workgroup's gate-to-up span of W) is addressed through one
+  // 32-bit buffer range that must stay below the out-of-range offset
+  if (static_cast<long long>(N) * K * 2 >= static_cast<long long>(kOutOfRange) ||
+      static_cast<long long>(rows) * K * 2 >= static_cast<long long>(kOutOfRange))
+    return fail(kNotSupported, "%s: operand over 2 GiB (rows=%d N=%d K=%d)", name, rows, N, K);
   const int cu = current_cu_count();
   if (cu <= 0) return fail(kInvalidValue, "%s: no device", name);
-  const DenseShape shape = pick_shape(M, N, cu);
-  const int mr = shape.mr, rb = shape.rb;
+  const int mr = SWIGLU ? 2 : (M % 32 == 0 ? 2 : 1);
+  const int gx = SWIGLU ? M / 16 : M / (16 * mr);
+  const int rb = pick_token_blocks(gx, N, cu);
   const int ny = ceil_div(N, 16 * rb);
   if (ny > 65535) return fail(kNotSupported, "%s: too many token blocks (N=%d)", name, N);
-  const dim3 grid(M / (16 * mr), ny);
+  const dim3 grid(gx, ny);
+  const int stride = SWIGLU ? M : 16;
   // Few workgroups: more waves each, splitting K (at least one step a wave).
   const long long wgs = static_cast<long long>(grid.x) * grid.y;
   int wk = wgs <= cu ? 16 : (wgs <= 2LL * cu ? 8 : 4);
   while (wk > 1 && K / 32 < wk) wk >>= 1;
   switch (wk) {
-    case 16: launch_dense<16>(mr, rb, grid, W, X, Y, M, N, K, stream); break;
-    case 8: launch_dense<8>(mr, rb, grid, W, X, Y, M, N, K, stream); break;
-    case 4: launch_dense<4>(mr, rb, grid, W, X, Y, M, N, K, stream); break;
-    case 2: launch_dense<2>(mr, rb, grid, W, X, Y, M, N, K, stream); break;
-    default: launch_dense<1>(mr, rb, grid, W, X, Y, M, N, K, stream); break;
+    case 16: launch_dense<16, SWIGLU>(mr, rb, grid, W, X, Y, M, N, K, stride, stream); break;
+    case 8: launch_dense<8, SWIGLU>(mr, rb, grid, W, X, Y, M, N, K, stride, stream); break;
+    case 4: launch_dense<4, SWIGLU>(mr, rb, grid, W, X, Y, M, N, K, stride, stream); break;
+    case 2: launch_dense<2, SWIGLU>(mr, rb, grid, W, X, Y, M, N, K, stride, stream); break;
+    default: launch_dense<1, SWIGLU>(mr, rb, grid, W, X, Y, M, N, K, stride, stream); break;
   }
   return launch_status(name);
 }
@@ -265,10 +286,19 @@ using namespace pega;
 // library's version never allocates, so both are graph-safe.
 PEGA_API int gemm_cuda(const uint16_t* W, const uint16_t* X, uint16_t* Y, int M, int N, int K,
                        hipStream_t stream) {
-  return dense_gemm(W, X, Y, M, N, K, stream, "gemm_cuda");
+  return dense_launch<false>(W, X, Y, M, M, N, K, stream, "gemm_cuda");
 }
 
 PEGA_API int gemm_graphsafe_cuda(const uint16_t* W, const uint16_t* X, uint16_t* Y, int M, int N,
                                  int K, hipStream_t stream) {
-  return dense_gemm(W, X, Y, M, N, K, stream, "gemm_graphsafe_cuda");
+  return dense_launch<false>(W, X, Y, M, M, N, K, stream, "gemm_graphsafe_cuda");
+}
+
+// No reference counterpart as one symbol: the shared expert's gate/up GEMM
+// followed by the SwiGLU of its bf16 output (moe_nccl.rs:107-123 runs
+// gemm_graphsafe_cuda then kimi_marlin_w13_swiglu_cuda), with the same bits.
+PEGA_API int pega_dense_w13_swiglu(const uint16_t* W13, const uint16_t* X, uint16_t* act,
+                                   int inter, int N, int K, hipStream_t stream) {
+  if (inter > (1 << 29)) return fail(kInvalidValue, "pega_dense_w13_swiglu: bad inter=%d", inter);
+  return dense_launch<true>(W13, X, act, 2 * inter, inter, N, K, stream, "pega_dense_w13_swiglu");
 }

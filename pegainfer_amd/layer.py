@@ -171,7 +171,9 @@ class DenseW4A16:
 
 class KimiSharedExpert:
     """The Kimi-K2 shared expert, a bf16 dense MLP (moe_nccl.rs:107-123): gate/up
-    GEMM [2I, H] -> SwiGLU (gate first) -> down GEMM [H, I], bf16 `projected` out."""
+    GEMM [2I, H] -> SwiGLU (gate first) -> down GEMM [H, I], bf16 `projected` out.
+    The gate/up GEMM and the SwiGLU run as one launch (dense_w13_swiglu, the same
+    bits as the reference's two calls)."""
 
     def __init__(self, gate_up: torch.Tensor, down: torch.Tensor, *, max_tokens: int,
                  device="cuda"):
@@ -181,13 +183,11 @@ class KimiSharedExpert:
         self.H = gate_up.shape[1]
         assert tuple(down.shape) == (self.H, self.I)
         bf = dict(dtype=torch.bfloat16, device=device)
-        self.gu = torch.zeros(max_tokens, 2 * self.I, **bf)
         self.act = torch.zeros(max_tokens, self.I, **bf)
 
     def forward(self, normed: torch.Tensor, projected: torch.Tensor) -> torch.Tensor:
         T = normed.shape[0]
-        ops.gemm_graphsafe(self.gate_up, normed, self.gu[:T])
-        ops.kimi_marlin_w13_swiglu(self.gu[:T], self.act[:T], T, self.I)
+        ops.dense_w13_swiglu(self.gate_up, normed, self.act[:T])
         ops.gemm_graphsafe(self.down, self.act[:T], projected)
         return projected
 

@@ -584,6 +584,22 @@ def gemm_graphsafe(w: torch.Tensor, x: torch.Tensor, y: torch.Tensor) -> None:
     _lib.call("gemm_graphsafe_cuda", _ptr(w), _ptr(x), _ptr(y), M, N, K, _stream())
 
 
+def dense_w13_swiglu(w13: torch.Tensor, x: torch.Tensor, act: torch.Tensor) -> None:
+    """act = SwiGLU(bf16(X * W13^T)) in one launch: W13 [2I, K] bf16 (gate rows
+    first), X [N, K], act [N, I].  The same bits as gemm_graphsafe followed by
+    kimi_marlin_w13_swiglu, the pair moe_nccl.rs:107-123 runs for the shared expert."""
+    _ensure(_is_bf16(w13) and _is_bf16(x) and _is_bf16(act), "dense SwiGLU operands must be bf16")
+    _ensure(w13.dim() == 2 and x.dim() == 2 and act.dim() == 2,
+            "dense SwiGLU operands must be 2-D")
+    _ensure(w13.is_contiguous() and x.is_contiguous() and act.is_contiguous(),
+            "dense SwiGLU operands must be contiguous")
+    two_i, K = w13.shape
+    N = x.shape[0]
+    _ensure(two_i % 2 == 0 and x.shape[1] == K, "dense SwiGLU shape mismatch")
+    _ensure(tuple(act.shape) == (N, two_i // 2), "dense SwiGLU output shape mismatch")
+    _lib.call("pega_dense_w13_swiglu", _ptr(w13), _ptr(x), _ptr(act), two_i // 2, N, K, _stream())
+
+
 # --------------------------------------------------------------------------
 # Routing select
 # --------------------------------------------------------------------------

@@ -109,3 +109,35 @@ def test_kimi_decode_layer_with_shared_expert(oracle):
     # the join itself is exact given its inputs
     assert np.array_equal(host(out), oracle.residual_add_scaled_f32(
         hidden, host(moe.projected), host(moe.routed_f32), ops.KIMI_K2_ROUTER_SCALE))
+
+
+@pytest.mark.parametrize("I,N,K", [(2048, 64, 7168), (256, 24, 1024), (48, 7, 96), (16, 100, 64)])
+def test_dense_w13_swiglu_equals_gemm_then_swiglu(oracle, I, N, K):
+    """The fused launch against the two-call chain it replaces (gate/up GEMM to
+    bf16, then the reference SwiGLU): the same bits.  The chain's GEMM is checked
+    against the oracle above and its SwiGLU bit-exactly elsewhere."""
+    from pegainfer_amd import ops
+    g = np.random.default_rng(I * 31 + N * 5 + K)
+    w = dev(oracle.f32_to_bf16((g.standard_normal((2 * I, K)) * 0.02).astype(np.float32)))
+    x = dev(oracle.f32_to_bf16(g.standard_normal((N, K)).astype(np.float32)))
+    w, x = w.view(torch.bfloat16), x.view(torch.bfloat16)
+    gu = torch.zeros(N, 2 * I, dtype=torch.bfloat16, device="cuda")
+    ops.gemm_graphsafe(w, x, gu)
+    chain = torch.zeros(N, I, dtype=torch.bfloat16, device="cuda")
+    ops.kimi_marlin_w13_swiglu(gu, chain, N, I)
+    fused = torch.full((N, I), float("nan"), dtype=torch.bfloat16, device="cuda")
+    ops.dense_w13_swiglu(w, x, fused)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(fused), host(chain)), (I, N, K)
+
+
+def test_dense_w13_swiglu_rejects():
+    from pegainfer_amd import _lib
+    L = _lib.lib()
+    s = torch.cuda.current_stream().cuda_stream
+    buf = torch.zeros(4096, dtype=torch.bfloat16, device="cuda")
+    p = ctypes.c_void_p(buf.data_ptr())
+    assert L.pega_dense_w13_swiglu(p, p, p, 24, 4, 64, s) == 801   # inter % 16
+    assert L.pega_dense_w13_swiglu(p, p, p, 16, 4, 48, s) == 801   # K % 32
+    assert L.pega_dense_w13_swiglu(None, p, p, 16, 4, 64, s) == 1
+    torch.cuda.synchronize()
