@@ -226,6 +226,21 @@ int kimi_residual_add_scaled_bf16_cuda(const uint16_t* hidden, const uint16_t* p
 int kimi_add_f32_bf16_to_bf16_cuda(const float* a, const uint16_t* b, uint16_t* out, int n,
                                    hipStream_t stream);
 
+/* Replaces f32_to_bf16_cuda, pegainfer-kernels/src/ffi/shared.rs:849-854
+ * (csrc/shared/elementwise.cu:235-244,722-728): out = bf16(input), round to nearest even. */
+int f32_to_bf16_cuda(const float* input, uint16_t* output, int n, hipStream_t stream);
+
+/* Replaces add_cuda, pegainfer-kernels/src/ffi/shared.rs:27-33
+ * (csrc/shared/elementwise.cu:9-21,500-507): out = bf16(f(a) + f(b)). */
+int add_cuda(const uint16_t* a, const uint16_t* b, uint16_t* out, int n, hipStream_t stream);
+
+/* No reference symbol of its own: the DeepSeek-V2-Lite routed + shared join,
+ * f32_to_bf16_cuda(routed) then add_cuda(., shared) as
+ * pegainfer-deepseek-v2-lite/src/nccl_backend.rs:544-545 and runtime/moe.rs:656 run them,
+ * in one pass with the same two roundings: out = bf16(f(bf16(routed)) + f(shared)). */
+int pega_moe_join_routed_shared_bf16(const float* routed, const uint16_t* shared, uint16_t* out,
+                                     int n, hipStream_t stream);
+
 /* ---------------- dense bf16 GEMM (shared expert) ----------------
  * Y[n][m] = bf16(sum_k W[m][k] * X[n][k]) with fp32 accumulation; W [M][K],
  * X [N][K], Y [N][M] bf16 row-major (the reference's cublasGemmEx(OP_T, OP_N)
@@ -250,6 +265,19 @@ int pega_dense_w13_swiglu(const uint16_t* W13, const uint16_t* X, uint16_t* act,
                           int K, hipStream_t stream);
 
 /* ---------------- routing select ---------------- */
+
+/* Replaces kimi_k2_router_noaux_tc_cuda, pegainfer-kernels/src/ffi/kimi.rs:52-66
+ * (csrc/kimi_k2/kimi_router.cu:108-187): logits [padded_tokens][n_experts] fp32 =
+ * hidden [padded_tokens][hidden_dim] . gate_weight [n_experts][hidden_dim]^T (fp32
+ * accumulation), then the select stage below over the first active_tokens rows.  Same
+ * rejections as the reference (1: null pointers, token counts, n_experts != 384,
+ * topk != 8, route_scale <= 0); 801 when hidden_dim % 32 != 0 or hidden / gate_weight are
+ * not 16-byte aligned. */
+int kimi_k2_router_noaux_tc_cuda(const uint16_t* hidden, const uint16_t* gate_weight,
+                                 const float* e_score_correction_bias, float* logits,
+                                 float* topk_weight, int32_t* topk_idx, int active_tokens,
+                                 int padded_tokens, int hidden_dim, int n_experts, int topk,
+                                 float route_scale, hipStream_t stream);
 
 /* No reference symbol of its own: the select stage (sigmoid, top-k of score+bias, renormalise)
  * of kimi_k2_router_noaux_tc_cuda, pegainfer-kernels/src/ffi/kimi.rs:52-66

@@ -370,6 +370,129 @@ int oracle_wna16_gemm(const uint16_t *input, uint16_t *output, const uint8_t *qw
 }
 
 /* ------------------------------------------------------------------------ */
+/* CPU BASELINE ONLY (bench.py's cpu_baseline leg), not a checker: the same  */
+/* grouped GEMM contract as oracle_wna16_gemm (dequant w = bf16((q-8)*s),     */
+/* fp32 products, bf16 output, bf16 top-k weight multiply) with the fp32 sum */
+/* of each output split into 16 lane sums that are added in a fixed tree     */
+/* order at the end, so the compiler can vectorise the dot products and the  */
+/* dequant.  target_clones builds AVX-512, AVX2 and baseline versions, picked */
+/* at load time for the host CPU.  Checked against oracle_wna16_gemm (bit   */
+/* for bit where every partial sum is exact, within the fp32 bound           */
+/* otherwise) in tests/test_oracle.py.                                       */
+/* ------------------------------------------------------------------------ */
+#define CLONES __attribute__((target_clones("avx512f", "avx2", "default")))
+
+CLONES static void dequant_col_fast(const uint8_t *q, const uint16_t *sc, int K, int G,
+                                    float *w) {
+  for (int g = 0; g < K / G; ++g) {
+    const float s = bf(sc[g]);
+    const uint8_t *qg = q + (size_t)g * (G / 2);
+    float *wg = w + (size_t)g * G;
+    for (int j = 0; j < G / 2; ++j) {
+      const float lo = (float)((int)(qg[j] & 15) - 8) * s;
+      const float hi = (float)((int)(qg[j] >> 4) - 8) * s;
+      uint32_t ul, uh;
+      memcpy(&ul, &lo, 4);
+      memcpy(&uh, &hi, 4);
+      ul = (ul + 0x7fffu + ((ul >> 16) & 1u)) & 0xffff0000u; /* finite: no NaN case */
+      uh = (uh + 0x7fffu + ((uh >> 16) & 1u)) & 0xffff0000u;
+      memcpy(&wg[2 * j], &ul, 4);
+      memcpy(&wg[2 * j + 1], &uh, 4);
+    }
+  }
+}
+
+CLONES static float dot16(const float *a, const float *w, int K) {
+  float acc[16] = {0};
+  int k = 0;
+  for (; k + 16 <= K; k += 16)
+    for (int j = 0; j < 16; ++j) acc[j] += a[k + j] * w[k + j];
+  for (; k < K; ++k) acc[k & 15] += a[k] * w[k];
+  for (int st = 8; st > 0; st >>= 1)
+    for (int j = 0; j < st; ++j) acc[j] += acc[j + st];
+  return acc[0];
+}
+
+static void gemm_block_fast(gemm_job *j, int mb, int n0, int n1, float *wcol, float *arows) {
+  const int K = j->size_k, G = j->group_size, kg = K / G;
+  const int ntp = j->num_tokens_post_padded[0];
+  if (mb * j->moe_block_size >= ntp) return;
+  int ex = j->expert_ids[mb];
+  if (ex < 0) return;
+  const size_t e_w = (size_t)j->size_n * (K / 2), e_s = (size_t)j->size_n * kg;
+  const int valid_limit = j->size_m * j->top_k;
+  int sids[64], nrows = 0;
+  for (int i = 0; i < j->moe_block_size && i < 64; ++i) {
+    int sid = j->sorted_token_ids[mb * j->moe_block_size + i];
+    if (sid >= valid_limit) continue;
+    const uint16_t *a = j->input + (size_t)(sid / j->top_k) * K;
+    float *ar = arows + (size_t)nrows * K;
+    for (int k = 0; k < K; ++k) ar[k] = bf(a[k]);
+    sids[nrows++] = sid;
+  }
+  if (nrows == 0) return;
+  for (int n = n0; n < n1; ++n) {
+    dequant_col_fast(j->qweight + ex * e_w + (size_t)n * (K / 2), j->scales + ex * e_s +
+                     (size_t)n * kg, K, G, wcol);
+    for (int r = 0; r < nrows; ++r) {
+      uint16_t c = to_bf(dot16(arows + (size_t)r * K, wcol, K));
+      if (j->mul_topk_weights) c = to_bf(bf(c) * bf(to_bf(j->topk_weights[sids[r]])));
+      j->output[(size_t)sids[r] * j->size_n + n] = c;
+    }
+  }
+}
+
+static void *gemm_worker_fast(void *arg) {
+  gemm_job *j = (gemm_job *)arg;
+  float *wcol = (float *)malloc(sizeof(float) * (size_t)j->size_k);
+  float *arows = (float *)malloc(sizeof(float) * (size_t)j->size_k * 64);
+  const int n_chunks = (j->size_n + j->n_chunk - 1) / j->n_chunk;
+  for (;;) {
+    pthread_mutex_lock(&j->lock);
+    int item = j->next_item++;
+    pthread_mutex_unlock(&j->lock);
+    if (item >= j->n_items) break;
+    int mb = item / n_chunks, nc = item % n_chunks;
+    int n0 = nc * j->n_chunk, n1 = n0 + j->n_chunk;
+    if (n1 > j->size_n) n1 = j->size_n;
+    gemm_block_fast(j, mb, n0, n1, wcol, arows);
+  }
+  free(wcol);
+  free(arows);
+  return NULL;
+}
+
+int oracle_wna16_gemm_fast(const uint16_t *input, uint16_t *output, const uint8_t *qweight,
+                           const uint16_t *scales, const int32_t *sorted_token_ids,
+                           const int32_t *expert_ids, const int32_t *num_tokens_post_padded,
+                           const float *topk_weights, int max_m_blocks, int moe_block_size,
+                           int top_k, int mul_topk_weights, int size_m, int size_n, int size_k,
+                           int group_size, int threads) {
+  if (size_k % group_size || size_k % 2 || group_size % 2 || moe_block_size > 64) return 1;
+  gemm_job j;
+  memset(&j, 0, sizeof(j));
+  j.input = input; j.output = output; j.qweight = qweight; j.scales = scales;
+  j.sorted_token_ids = sorted_token_ids; j.expert_ids = expert_ids;
+  j.num_tokens_post_padded = num_tokens_post_padded; j.topk_weights = topk_weights;
+  j.moe_block_size = moe_block_size; j.top_k = top_k; j.mul_topk_weights = mul_topk_weights;
+  j.size_m = size_m; j.size_n = size_n; j.size_k = size_k; j.group_size = group_size;
+  j.n_chunk = 64;
+  j.n_items = max_m_blocks * ((size_n + j.n_chunk - 1) / j.n_chunk);
+  pthread_mutex_init(&j.lock, NULL);
+  if (threads < 1) threads = 1;
+  if (threads == 1) {
+    gemm_worker_fast(&j);
+  } else {
+    pthread_t *tid = (pthread_t *)malloc(sizeof(pthread_t) * threads);
+    for (int t = 0; t < threads; ++t) pthread_create(&tid[t], NULL, gemm_worker_fast, &j);
+    for (int t = 0; t < threads; ++t) pthread_join(tid[t], NULL);
+    free(tid);
+  }
+  pthread_mutex_destroy(&j.lock);
+  return 0;
+}
+
+/* ------------------------------------------------------------------------ */
 /* K3: SwiGLU (kimi_marlin_wna16.cu:345-361):                                */
 /*   out = bf16( f(bf16( g/(1+exp(-g)) )) * u ),  g = w13[r,c], u = w13[r,I+c] */
 /* Pinned by: fp64 evaluation of the same closed form (agreement to 1 bf16   */
@@ -420,6 +543,50 @@ int oracle_dense_gemm(const uint16_t *W, const uint16_t *X, uint16_t *Y, int M, 
   }
   free(wrow);
   free(xrow);
+  return 0;
+}
+
+/* Router logits GEMM of kimi_k2_router_noaux_tc (pegainfer-kernels/csrc/kimi_k2/      */
+/* kimi_router.cu:108-142: cublasGemmEx(OP_T, OP_N, n_experts, padded_tokens,         */
+/* hidden_dim, gate lda hidden_dim, hidden ldb hidden_dim, logits CUDA_R_32F ldc       */
+/* n_experts, CUBLAS_COMPUTE_32F_PEDANTIC)):                                          */
+/*   Y[n][m] = sum_k f(W[m][k]) * f(X[n][k])  in fp32, NOT rounded to bf16            */
+/* (k ascending here; parity to the fp32-accumulation bound).  Pinned by: small-      */
+/* integer operands whose every partial sum is exact (any order gives these bits),   */
+/* one-hot rows of X (Y is a row of W exactly), bf16(Y) == oracle_dense_gemm, and an  */
+/* fp64 bound on random operands.                                                    */
+int oracle_dense_gemm_f32(const uint16_t *W, const uint16_t *X, float *Y, int M, int N, int K) {
+  if (M <= 0 || N <= 0 || K <= 0) return 1;
+  float *xrow = (float *)malloc(sizeof(float) * (size_t)K);
+  if (!xrow) return 2;
+  for (int n = 0; n < N; ++n) {
+    for (int k = 0; k < K; ++k) xrow[k] = bf(X[(size_t)n * K + k]);
+    for (int m = 0; m < M; ++m) {
+      const uint16_t *w = W + (size_t)m * K;
+      float acc = 0.0f;
+      for (int k = 0; k < K; ++k) acc += bf(w[k]) * xrow[k];
+      Y[(size_t)n * M + m] = acc;
+    }
+  }
+  free(xrow);
+  return 0;
+}
+
+/* f32_to_bf16_cuda (pegainfer-kernels/csrc/shared/elementwise.cu:235-244):           */
+/* out = bf16(x), round to nearest even.  Pinned by: numpy's independent rounding     */
+/* (tests) and the tie cases 1 + 2^-8 -> 1, 1 + 3*2^-8 -> 1 + 2^-6.                    */
+int oracle_f32_to_bf16_n(const float *x, uint16_t *out, int n) {
+  for (int i = 0; i < n; ++i) out[i] = to_bf(x[i]);
+  return 0;
+}
+
+/* add_cuda / add_kernel (pegainfer-kernels/csrc/shared/elementwise.cu:9-21):          */
+/* out = bf16(f(a) + f(b)).  With oracle_f32_to_bf16_n first it is the DeepSeek-V2-   */
+/* Lite routed + shared join (nccl_backend.rs:544-545, runtime/moe.rs:656).  Pinned  */
+/* by: numpy float32 addition and rounding, and inputs on which the join's two        */
+/* roundings differ from one rounding of routed + shared.                             */
+int oracle_add_bf16(const uint16_t *a, const uint16_t *b, uint16_t *out, int n) {
+  for (int i = 0; i < n; ++i) out[i] = to_bf(bf(a[i]) + bf(b[i]));
   return 0;
 }
 

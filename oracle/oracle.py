@@ -43,6 +43,10 @@ def lib():
             "oracle_marlin_reorder_scale": [_P, _P, _I, _I, _I, _I],
             "oracle_marlin_fuse_w13": [_P] * 6 + [_I] * 4,
             "oracle_wna16_gemm": [_P] * 8 + [_I] * 9,
+            "oracle_wna16_gemm_fast": [_P] * 8 + [_I] * 9,
+            "oracle_dense_gemm_f32": [_P, _P, _P, _I, _I, _I],
+            "oracle_f32_to_bf16_n": [_P, _P, _I],
+            "oracle_add_bf16": [_P, _P, _P, _I],
             "oracle_swiglu": [_P, _P, _I, _I],
             "oracle_dense_gemm": [_P, _P, _P, _I, _I, _I],
             "oracle_sum_topk_rows": [_P, _P, _I, _I, _I],
@@ -175,9 +179,11 @@ def marlin_fuse_w13(gate_w, up_w, gate_s, up_s, in_dim, inter, local_experts, gr
 # ---------------------------------------------------------------- GEMM
 def wna16_gemm(input_bf16, qweight_ckpt_u8, scales_ckpt_bf16, routing, topk_weights, *,
                moe_block_size, top_k, mul_topk_weights, size_m, size_n, size_k,
-               group_size=32, output=None, threads=1):
+               group_size=32, output=None, threads=1, fast=False):
     """C[sorted_id, :] for every valid routed row; other rows of ``output`` are
-    left as given (zeros by default, as the reference's caller zero-fills)."""
+    left as given (zeros by default, as the reference's caller zero-fills).
+    fast=True runs the vectorised CPU-baseline variant (16 lane sums per dot
+    product) instead of the k-ascending checker."""
     a = np.ascontiguousarray(input_bf16, dtype=np.uint16)
     qw = np.ascontiguousarray(qweight_ckpt_u8, dtype=np.uint8)
     sc = np.ascontiguousarray(scales_ckpt_bf16, dtype=np.uint16)
@@ -188,7 +194,8 @@ def wna16_gemm(input_bf16, qweight_ckpt_u8, scales_ckpt_bf16, routing, topk_weig
     if output is None:
         output = np.zeros((size_m * top_k, size_n), np.uint16)
     assert output.flags["C_CONTIGUOUS"] and output.dtype == np.uint16
-    _check(lib().oracle_wna16_gemm(
+    fn = lib().oracle_wna16_gemm_fast if fast else lib().oracle_wna16_gemm
+    _check(fn(
         _ptr(a), _ptr(output), _ptr(qw), _ptr(sc), _ptr(st), _ptr(ei), _ptr(ntp), _ptr(tw),
         ei.size, moe_block_size, top_k, int(bool(mul_topk_weights)), size_m, size_n, size_k,
         group_size, threads), "wna16_gemm")
@@ -209,7 +216,52 @@ def dense_gemm(w_bf16, x_bf16):
     return y
 
 
+def dense_gemm_f32(w_bf16, x_bf16):
+    """Y[n][m] = sum_k W[m][k] X[n][k] in fp32, unrounded (the Kimi router's logits
+    GEMM, kimi_router.cu:108-142); W [M, K], X [N, K] -> Y [N, M] float32."""
+    w = np.ascontiguousarray(w_bf16, dtype=np.uint16)
+    x = np.ascontiguousarray(x_bf16, dtype=np.uint16)
+    M, K = w.shape
+    N = x.shape[0]
+    assert x.shape[1] == K
+    y = np.empty((N, M), np.float32)
+    _check(lib().oracle_dense_gemm_f32(_ptr(w), _ptr(x), _ptr(y), M, N, K), "dense_gemm_f32")
+    return y
+
+
+def kimi_router_noaux_tc(hidden_bf16, gate_bf16, bias, topk=8, route_scale=1.0):
+    """kimi_k2_router_noaux_tc_cuda (kimi_router.cu:148-187): fp32 logits of all
+    rows, then the select stage.  Returns (logits, topk_idx, topk_weight)."""
+    logits = dense_gemm_f32(gate_bf16, hidden_bf16)
+    idx, w = kimi_router(logits, bias, topk=topk, route_scale=route_scale)
+    return logits, idx, w
+
+
 # ---------------------------------------------------------------- elementwise
+def f32_to_bf16_n(x_f32):
+    """f32_to_bf16_cuda (shared/elementwise.cu:235-244) through the C restatement."""
+    x = np.ascontiguousarray(x_f32, dtype=np.float32)
+    out = np.empty(x.shape, np.uint16)
+    _check(lib().oracle_f32_to_bf16_n(_ptr(x), _ptr(out), x.size), "f32_to_bf16")
+    return out
+
+
+def add_bf16(a_bf16, b_bf16):
+    """add_cuda (shared/elementwise.cu:9-21): bf16(f(a) + f(b))."""
+    a = np.ascontiguousarray(a_bf16, dtype=np.uint16)
+    b = np.ascontiguousarray(b_bf16, dtype=np.uint16)
+    assert a.shape == b.shape
+    out = np.empty(a.shape, np.uint16)
+    _check(lib().oracle_add_bf16(_ptr(a), _ptr(b), _ptr(out), a.size), "add_bf16")
+    return out
+
+
+def dsv2_join(routed_f32, shared_bf16):
+    """DeepSeek-V2-Lite routed + shared join as the reference runs it: the fp32
+    routed sum to bf16 (f32_to_bf16_hidden_into, nccl_backend.rs:544-545), then
+    the bf16 add (add_batch_into, runtime/moe.rs:656)."""
+    return add_bf16(f32_to_bf16_n(routed_f32), shared_bf16)
+
 def swiglu(w13_bf16, inter):
     w = np.ascontiguousarray(w13_bf16, dtype=np.uint16)
     rows = w.size // (2 * inter)
@@ -292,7 +344,7 @@ def expf(x: float) -> float:
 # ---------------------------------------------------------------- composites
 def kimi_moe_layer(hidden_bf16, qw13_ckpt, s13_ckpt, qw2_ckpt, s2_ckpt, topk_idx, topk_w, *,
                    global_start, local_experts, block_size, hidden, inter, topk=8,
-                   group_size=32, threads=1):
+                   group_size=32, threads=1, fast=False):
     """The routed-expert sequence of pegainfer-kimi-k2/src/runner/moe_nccl.rs:152-203:
     align -> W13 (top_k=topk, no weight mul) -> SwiGLU -> W2 (top_k=1, weight mul)
     -> fp32 top-k row sum.  W13 checkpoint weights are the fused [E, 2I, H/2]
@@ -303,10 +355,10 @@ def kimi_moe_layer(hidden_bf16, qw13_ckpt, s13_ckpt, qw2_ckpt, s2_ckpt, topk_idx
     w13 = wna16_gemm(hidden_bf16, qw13_ckpt, s13_ckpt, routing, topk_w,
                      moe_block_size=block_size, top_k=topk, mul_topk_weights=False,
                      size_m=tokens, size_n=2 * inter, size_k=hidden, group_size=group_size,
-                     threads=threads)
+                     threads=threads, fast=fast)
     act = swiglu(w13, inter)
     out = wna16_gemm(act, qw2_ckpt, s2_ckpt, routing, topk_w, moe_block_size=block_size,
                      top_k=1, mul_topk_weights=True, size_m=route_elems, size_n=hidden,
-                     size_k=inter, group_size=group_size, threads=threads)
+                     size_k=inter, group_size=group_size, threads=threads, fast=fast)
     routed = sum_topk_rows(out, tokens, topk, hidden)
     return routed, dict(routing=routing, w13=w13, act=act, route_out=out)

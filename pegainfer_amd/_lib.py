@@ -54,7 +54,11 @@ SIGNATURES = {
     "kimi_residual_add_scaled_f32_cuda": [_P, _P, _P, _F, _P, _I, _P],
     "kimi_residual_add_scaled_bf16_cuda": [_P, _P, _P, _F, _P, _I, _P],
     "kimi_add_f32_bf16_to_bf16_cuda": [_P, _P, _P, _I, _P],
+    "f32_to_bf16_cuda": [_P, _P, _I, _P],
+    "add_cuda": [_P, _P, _P, _I, _P],
+    "pega_moe_join_routed_shared_bf16": [_P, _P, _P, _I, _P],
     "pega_kimi_router_select": [_P, _P, _P, _P, _I, _I, _I, _F, _P],
+    "kimi_k2_router_noaux_tc_cuda": [_P] * 6 + [_I] * 5 + [_F, _P],
     "pega_dsv2_router_select": [_P, _P, _P, _I, _I, _I, _P],
     "pega_wna16_prefill_pair": [ctypes.POINTER(Wna16Problem), ctypes.POINTER(Wna16Problem), _P],
     "gemm_cuda": [_P, _P, _P, _I, _I, _I, _P],

@@ -34,6 +34,11 @@ int launch_status(const char* what);
 // Number of compute units of the current device (cached per device).
 int current_cu_count();
 
+// Y[n][m] = sum_k f(W[m][k]) * f(X[n][k]) in fp32, unrounded: W [M][K], X [N][K] bf16,
+// Y [N][M] fp32 (dense.hip; the router's logits GEMM).  Returns a Status.
+int dense_gemm_f32(const uint16_t* W, const uint16_t* X, float* Y, int M, int N, int K,
+                   hipStream_t stream, const char* name);
+
 // ---------------------------------------------------------------- bf16 helpers
 __device__ __forceinline__ float bf2f(uint16_t h) {
   return __builtin_bit_cast(float, static_cast<uint32_t>(h) << 16);

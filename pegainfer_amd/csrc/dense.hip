@@ -70,13 +70,16 @@ struct StepRegs {
 // SWIGLU (MR = 2): tile 0 holds gate features m0..m0+15 and tile 1 the
 // matching up features (tile_stride = I); the epilogue rounds both sums to
 // bf16 as the GEMM's output would be, applies SwiGLU and writes act[n][m0+c]
-// (Y row stride M = I).
-template <int WK, int MR, int RB, bool SWIGLU>
+// (Y row stride M = I).  F32: Y is fp32 and takes the sums unrounded (the
+// router's logits GEMM, cublasGemmEx with CUDA_R_32F output).
+template <int WK, int MR, int RB, bool SWIGLU, bool F32 = false>
 __global__ __launch_bounds__(64 * WK) void dense_gemm_kernel(const uint16_t* __restrict__ W,
                                                              const uint16_t* __restrict__ X,
-                                                             uint16_t* __restrict__ Y, int M,
+                                                             void* __restrict__ Yv, int M,
                                                              int N, int K, int tile_stride) {
   static_assert(!SWIGLU || MR == 2, "SwiGLU pairs one gate and one up tile");
+  static_assert(!(SWIGLU && F32), "the SwiGLU epilogue writes bf16");
+  uint16_t* __restrict__ Y = static_cast<uint16_t*>(Yv);
   constexpr int D = MR + RB <= 5 ? 4 : 3;  // the ring fits 128 VGPRs at WK = 16
   __shared__ float s_red[WK][RB * 4][64];
   const int lane = threadIdx.x & 63;
@@ -195,31 +198,35 @@ __global__ __launch_bounds__(64 * WK) void dense_gemm_kernel(const uint16_t* __r
               swiglu_one(bf2f(f2bf(gsum[i])), bf2f(f2bf(sum)));
         }
       } else if (n < N) {
-        Y[static_cast<long long>(n) * M + m0 + 16 * mr + c] = f2bf(sum);
+        const long long o = static_cast<long long>(n) * M + m0 + 16 * mr + c;
+        if constexpr (F32)
+          static_cast<float*>(Yv)[o] = sum;
+        else
+          Y[o] = f2bf(sum);
       }
     }
   }
 }
 
-template <int WK, int MR, bool SWIGLU>
-void launch_dense_rb(int rb, dim3 grid, const uint16_t* W, const uint16_t* X, uint16_t* Y, int M,
+template <int WK, int MR, bool SWIGLU, bool F32>
+void launch_dense_rb(int rb, dim3 grid, const uint16_t* W, const uint16_t* X, void* Y, int M,
                      int N, int K, int stride, hipStream_t stream) {
   const dim3 block(64 * WK);
   switch (rb) {
-    case 1: hipLaunchKernelGGL((dense_gemm_kernel<WK, MR, 1, SWIGLU>), grid, block, 0, stream, W, X, Y, M, N, K, stride); break;
-    case 2: hipLaunchKernelGGL((dense_gemm_kernel<WK, MR, 2, SWIGLU>), grid, block, 0, stream, W, X, Y, M, N, K, stride); break;
-    case 3: hipLaunchKernelGGL((dense_gemm_kernel<WK, MR, 3, SWIGLU>), grid, block, 0, stream, W, X, Y, M, N, K, stride); break;
-    default: hipLaunchKernelGGL((dense_gemm_kernel<WK, MR, 4, SWIGLU>), grid, block, 0, stream, W, X, Y, M, N, K, stride); break;
+    case 1: hipLaunchKernelGGL((dense_gemm_kernel<WK, MR, 1, SWIGLU, F32>), grid, block, 0, stream, W, X, Y, M, N, K, stride); break;
+    case 2: hipLaunchKernelGGL((dense_gemm_kernel<WK, MR, 2, SWIGLU, F32>), grid, block, 0, stream, W, X, Y, M, N, K, stride); break;
+    case 3: hipLaunchKernelGGL((dense_gemm_kernel<WK, MR, 3, SWIGLU, F32>), grid, block, 0, stream, W, X, Y, M, N, K, stride); break;
+    default: hipLaunchKernelGGL((dense_gemm_kernel<WK, MR, 4, SWIGLU, F32>), grid, block, 0, stream, W, X, Y, M, N, K, stride); break;
   }
 }
 
-template <int WK, bool SWIGLU>
-void launch_dense(int mr, int rb, dim3 grid, const uint16_t* W, const uint16_t* X, uint16_t* Y,
+template <int WK, bool SWIGLU, bool F32>
+void launch_dense(int mr, int rb, dim3 grid, const uint16_t* W, const uint16_t* X, void* Y,
                   int M, int N, int K, int stride, hipStream_t stream) {
   if (SWIGLU || mr == 2)
-    launch_dense_rb<WK, 2, SWIGLU>(rb, grid, W, X, Y, M, N, K, stride, stream);
+    launch_dense_rb<WK, 2, SWIGLU, F32>(rb, grid, W, X, Y, M, N, K, stride, stream);
   else
-    launch_dense_rb<WK, 1, false>(rb, grid, W, X, Y, M, N, K, stride, stream);
+    launch_dense_rb<WK, 1, false, F32>(rb, grid, W, X, Y, M, N, K, stride, stream);
 }
 
 // Row tiles per wave: two where M allows (each X fragment then feeds two
@@ -238,8 +245,8 @@ int pick_token_blocks(long long row_groups, int N, int cu) {
 
 // Shared checks and launch.  rows = W rows read (M, or 2 I for SwiGLU),
 // M = output features per token row of Y.
-template <bool SWIGLU>
-int dense_launch(const uint16_t* W, const uint16_t* X, uint16_t* Y, int rows, int M, int N, int K,
+template <bool SWIGLU, bool F32 = false>
+int dense_launch(const uint16_t* W, const uint16_t* X, void* Y, int rows, int M, int N, int K,
                  hipStream_t stream, const char* name) {
   if (!W || !X || !Y) return fail(kInvalidValue, "%s: null pointer", name);
   if (M <= 0 || N <= 0 || K <= 0)
@@ -248,11 +255,15 @@ int dense_launch(const uint16_t* W, const uint16_t* X, uint16_t* Y, int rows, in
     return fail(kNotSupported, "%s: M %% 16 and K %% 32 must be 0 (M=%d K=%d)", name, M, K);
   if ((reinterpret_cast<uintptr_t>(W) & 15u) != 0 || (reinterpret_cast<uintptr_t>(X) & 15u) != 0)
     return fail(kInvalidValue, "%s: W and X must be 16-byte aligned", name);
-  // X (and a SwiGLU workgroup's gate-to-up span of W) is addressed through one
-  // 32-bit buffer range that must stay below the out-of-range offset
+  // X is addressed through one 32-bit buffer range that must stay below the
+  // out-of-range offset, and so is a workgroup's W span: its 16 MR rows, or
+  // with SwiGLU its gate rows through its up rows (I + 16 rows).  The size of
+  // W as a whole does not matter.
+  const long long w_span = SWIGLU ? static_cast<long long>(M) + 16 : 32;
   if (static_cast<long long>(N) * K * 2 >= static_cast<long long>(kOutOfRange) ||
-      static_cast<long long>(rows) * K * 2 >= static_cast<long long>(kOutOfRange))
-    return fail(kNotSupported, "%s: operand over 2 GiB (rows=%d N=%d K=%d)", name, rows, N, K);
+      w_span * K * 2 >= static_cast<long long>(kOutOfRange))
+    return fail(kNotSupported, "%s: operand span over 2 GiB (rows=%d N=%d K=%d)", name, rows, N,
+                K);
   const int cu = current_cu_count();
   if (cu <= 0) return fail(kInvalidValue, "%s: no device", name);
   const int mr = SWIGLU ? 2 : (M % 32 == 0 ? 2 : 1);
@@ -267,16 +278,23 @@ int dense_launch(const uint16_t* W, const uint16_t* X, uint16_t* Y, int rows, in
   int wk = wgs <= cu ? 16 : (wgs <= 2LL * cu ? 8 : 4);
   while (wk > 1 && K / 32 < wk) wk >>= 1;
   switch (wk) {
-    case 16: launch_dense<16, SWIGLU>(mr, rb, grid, W, X, Y, M, N, K, stride, stream); break;
-    case 8: launch_dense<8, SWIGLU>(mr, rb, grid, W, X, Y, M, N, K, stride, stream); break;
-    case 4: launch_dense<4, SWIGLU>(mr, rb, grid, W, X, Y, M, N, K, stride, stream); break;
-    case 2: launch_dense<2, SWIGLU>(mr, rb, grid, W, X, Y, M, N, K, stride, stream); break;
-    default: launch_dense<1, SWIGLU>(mr, rb, grid, W, X, Y, M, N, K, stride, stream); break;
+    case 16: launch_dense<16, SWIGLU, F32>(mr, rb, grid, W, X, Y, M, N, K, stride, stream); break;
+    case 8: launch_dense<8, SWIGLU, F32>(mr, rb, grid, W, X, Y, M, N, K, stride, stream); break;
+    case 4: launch_dense<4, SWIGLU, F32>(mr, rb, grid, W, X, Y, M, N, K, stride, stream); break;
+    case 2: launch_dense<2, SWIGLU, F32>(mr, rb, grid, W, X, Y, M, N, K, stride, stream); break;
+    default: launch_dense<1, SWIGLU, F32>(mr, rb, grid, W, X, Y, M, N, K, stride, stream); break;
   }
   return launch_status(name);
 }
 
 }  // namespace
+
+// The router's logits GEMM (fp32 output); declared in common.h.
+int dense_gemm_f32(const uint16_t* W, const uint16_t* X, float* Y, int M, int N, int K,
+                   hipStream_t stream, const char* name) {
+  return dense_launch<false, true>(W, X, Y, M, M, N, K, stream, name);
+}
+
 }  // namespace pega
 
 using namespace pega;

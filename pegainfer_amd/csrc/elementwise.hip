@@ -10,7 +10,11 @@
 //   kimi_add_f32_bf16_to_bf16_cuda        kimi_experts.cu:15-23,270-285
 //   pega_weighted_topk_sum_f32            dsv2_lite_moe.cu:131-155 (fmaf chain)
 //   pega_moe_combine_local_f32            either combine over local routes only
+//   f32_to_bf16_cuda                      shared/elementwise.cu:235-244,722-728
+//   add_cuda                              shared/elementwise.cu:9-21,500-507
+//   pega_moe_join_routed_shared_bf16      the two calls above in one pass
 #include "common.h"
+#include "pega_moe.h"
 
 namespace pega {
 namespace {
@@ -241,6 +245,56 @@ __global__ void add_f32_bf16_kernel(const float* __restrict__ a, const uint16_t*
     out[i] = f2bf(__fadd_rn(a[i], bf2f(b[i])));
 }
 
+// out = bf16(x)  (pegainfer-kernels/csrc/shared/elementwise.cu:235-244)
+__global__ void f32_to_bf16_kernel(const float* __restrict__ x, uint16_t* __restrict__ out,
+                                   long long n) {
+  for (long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<long long>(gridDim.x) * blockDim.x)
+    out[i] = f2bf(x[i]);
+}
+
+// out = bf16(f(a) + f(b))  (pegainfer-kernels/csrc/shared/elementwise.cu:9-21)
+__global__ void add_bf16_kernel(const uint16_t* __restrict__ a, const uint16_t* __restrict__ b,
+                                uint16_t* __restrict__ out, long long n) {
+  for (long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<long long>(gridDim.x) * blockDim.x)
+    out[i] = f2bf(__fadd_rn(bf2f(a[i]), bf2f(b[i])));
+}
+
+// The DeepSeek-V2-Lite routed + shared join as the reference rounds it: the
+// fp32 routed sum goes to bf16 first (f32_to_bf16_cuda, nccl_backend.rs:
+// 544-545), then the bf16 add (add_cuda via add_batch, runtime/moe.rs:656):
+//   out = bf16( f(bf16(routed)) + f(shared) ).
+// Eight elements per thread, 16-byte shared/out and 2 x 16-byte routed I/O.
+__global__ void join_routed_shared_vec_kernel(const float* __restrict__ routed,
+                                              const uint16_t* __restrict__ shared,
+                                              uint16_t* __restrict__ out, long long n8) {
+  for (long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; i < n8;
+       i += static_cast<long long>(gridDim.x) * blockDim.x) {
+    const float4 r0 = reinterpret_cast<const float4*>(routed)[2 * i];
+    const float4 r1 = reinterpret_cast<const float4*>(routed)[2 * i + 1];
+    const uint4 sv = reinterpret_cast<const uint4*>(shared)[i];
+    const float r[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
+    const uint32_t sw[4] = {sv.x, sv.y, sv.z, sv.w};
+    uint32_t ow[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint16_t lo = f2bf(__fadd_rn(bf2f(f2bf(r[2 * j])), bf_lo(sw[j])));
+      const uint16_t hi = f2bf(__fadd_rn(bf2f(f2bf(r[2 * j + 1])), bf_hi(sw[j])));
+      ow[j] = static_cast<uint32_t>(lo) | (static_cast<uint32_t>(hi) << 16);
+    }
+    reinterpret_cast<uint4*>(out)[i] = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+  }
+}
+
+__global__ void join_routed_shared_kernel(const float* __restrict__ routed,
+                                          const uint16_t* __restrict__ shared,
+                                          uint16_t* __restrict__ out, long long n) {
+  for (long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<long long>(gridDim.x) * blockDim.x)
+    out[i] = f2bf(__fadd_rn(bf2f(f2bf(routed[i])), bf2f(shared[i])));
+}
+
 constexpr int kThreads = 256;
 
 unsigned grid_cap(long long work, int cap) {
@@ -388,4 +442,45 @@ PEGA_API int kimi_add_f32_bf16_to_bf16_cuda(const float* a, const uint16_t* b, u
   hipLaunchKernelGGL(add_f32_bf16_kernel, dim3(grid_cap(n, 1 << 20)), dim3(kThreads), 0, stream,
                      a, b, out, static_cast<long long>(n));
   return launch_status("add_f32_bf16");
+}
+
+// Reference: pegainfer-kernels/src/ffi/shared.rs:849-854 (f32_to_bf16_cuda,
+// csrc/shared/elementwise.cu:722-728).
+PEGA_API int f32_to_bf16_cuda(const float* input, uint16_t* output, int n, hipStream_t stream) {
+  if (!input || !output || n < 0) return fail(kInvalidValue, "f32_to_bf16: bad arguments");
+  if (n == 0) return kSuccess;
+  hipLaunchKernelGGL(f32_to_bf16_kernel, dim3(grid_cap(n, 1 << 20)), dim3(kThreads), 0, stream,
+                     input, output, static_cast<long long>(n));
+  return launch_status("f32_to_bf16");
+}
+
+// Reference: pegainfer-kernels/src/ffi/shared.rs:27-33 (add_cuda,
+// csrc/shared/elementwise.cu:500-507).
+PEGA_API int add_cuda(const uint16_t* a, const uint16_t* b, uint16_t* out, int n,
+                      hipStream_t stream) {
+  if (!a || !b || !out || n < 0) return fail(kInvalidValue, "add: bad arguments");
+  if (n == 0) return kSuccess;
+  hipLaunchKernelGGL(add_bf16_kernel, dim3(grid_cap(n, 1 << 20)), dim3(kThreads), 0, stream, a, b,
+                     out, static_cast<long long>(n));
+  return launch_status("add");
+}
+
+// No reference symbol of its own: f32_to_bf16_cuda(routed) followed by
+// add_cuda(bf16 routed, shared), the DeepSeek-V2-Lite layer's routed + shared
+// join (nccl_backend.rs:544-545, runtime/moe.rs:656), in one pass with the
+// same two roundings.
+PEGA_API int pega_moe_join_routed_shared_bf16(const float* routed, const uint16_t* shared,
+                                              uint16_t* out, int n, hipStream_t stream) {
+  if (!routed || !shared || !out || n < 0)
+    return fail(kInvalidValue, "join_routed_shared: bad arguments");
+  if (n == 0) return kSuccess;
+  if (n % 8 == 0 && aligned16(routed) && aligned16(shared) && aligned16(out)) {
+    const long long n8 = n / 8;
+    hipLaunchKernelGGL(join_routed_shared_vec_kernel, dim3(grid_cap(n8, 1 << 20)),
+                       dim3(kThreads), 0, stream, routed, shared, out, n8);
+  } else {
+    hipLaunchKernelGGL(join_routed_shared_kernel, dim3(grid_cap(n, 1 << 20)), dim3(kThreads), 0,
+                       stream, routed, shared, out, static_cast<long long>(n));
+  }
+  return launch_status("join_routed_shared");
 }

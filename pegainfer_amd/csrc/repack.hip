@@ -19,6 +19,7 @@
 // Reference: pegainfer-kernels/csrc/kimi_k2/kimi_marlin_int4.cu:21-263;
 // Rust ops src/ops/kimi_k2/experts.rs:850-1022.
 #include "common.h"
+#include "pega_moe.h"
 
 namespace pega {
 namespace {
@@ -165,15 +166,22 @@ int fuse_w13(const uint8_t* gate_w, const uint8_t* up_w, uint8_t* w13_w, const u
 
 // ---------------------------------------------------------------- C ABI
 // Reference declarations: pegainfer-kernels/src/ffi/kimi.rs:68-101; guards
-// kimi_marlin_int4.cu:15-19,179-184,201-213,235-242 (local_experts == 48).
+// kimi_marlin_int4.cu:15-19,179-184,201-213,235-242 (local_experts == 48).  The
+// reference maps every failure of these calls, a launch failure included, to
+// CUDA_ERROR_INVALID_VALUE (kimi_marlin_int4.cu:190,220,254,262), and so do these.
+namespace {
+int as_invalid_value(int rc) { return rc == pega::kSuccess ? rc : pega::kInvalidValue; }
+}  // namespace
+
 PEGA_API int kimi_marlin_int4_reorder_weight_cuda(const uint8_t* weight_packed_checkpoint,
                                                   uint8_t* weight_packed_marlin, int in_dim,
                                                   int out_dim, int local_experts,
                                                   int group_size, hipStream_t stream) {
   if (local_experts != 48)
     return pega::fail(pega::kInvalidValue, "kimi reorder_weight: local_experts must be 48");
-  return pega::reorder_weight(weight_packed_checkpoint, weight_packed_marlin, in_dim, out_dim,
-                              local_experts, group_size, stream);
+  return as_invalid_value(pega::reorder_weight(weight_packed_checkpoint, weight_packed_marlin,
+                                               in_dim, out_dim, local_experts, group_size,
+                                               stream));
 }
 
 PEGA_API int kimi_marlin_int4_reorder_scale_cuda(const uint16_t* weight_scale_checkpoint,
@@ -182,8 +190,9 @@ PEGA_API int kimi_marlin_int4_reorder_scale_cuda(const uint16_t* weight_scale_ch
                                                  hipStream_t stream) {
   if (local_experts != 48)
     return pega::fail(pega::kInvalidValue, "kimi reorder_scale: local_experts must be 48");
-  return pega::reorder_scale(weight_scale_checkpoint, weight_scale_marlin, in_dim, out_dim,
-                             local_experts, group_size, stream);
+  return as_invalid_value(pega::reorder_scale(weight_scale_checkpoint, weight_scale_marlin,
+                                              in_dim, out_dim, local_experts, group_size,
+                                              stream));
 }
 
 PEGA_API int kimi_marlin_int4_fuse_w13_cuda(const uint8_t* gate_weight_packed_marlin,
@@ -196,10 +205,10 @@ PEGA_API int kimi_marlin_int4_fuse_w13_cuda(const uint8_t* gate_weight_packed_ma
                                             int group_size, hipStream_t stream) {
   if (local_experts != 48)
     return pega::fail(pega::kInvalidValue, "kimi fuse_w13: local_experts must be 48");
-  return pega::fuse_w13(gate_weight_packed_marlin, up_weight_packed_marlin,
-                        w13_weight_packed_marlin, gate_scale_marlin, up_scale_marlin,
-                        w13_scale_marlin, in_dim, intermediate_dim, local_experts, group_size,
-                        stream);
+  return as_invalid_value(pega::fuse_w13(gate_weight_packed_marlin, up_weight_packed_marlin,
+                                         w13_weight_packed_marlin, gate_scale_marlin,
+                                         up_scale_marlin, w13_scale_marlin, in_dim,
+                                         intermediate_dim, local_experts, group_size, stream));
 }
 
 // Shape-general variants (any expert count; no reference counterpart).

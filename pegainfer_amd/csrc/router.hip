@@ -4,8 +4,11 @@
 //   pega_kimi_router_select   sigmoid scores, top-k of score + bias (ties ->
 //       lower id) kept in selection order, weight = score * (scale / sum).
 //       Reference: pegainfer-kernels/csrc/kimi_k2/kimi_router.cu:20-91
-//       (router_scores_topk_normalize_kernel; the logits GEMM before it,
-//       :108-142, is cuBLAS and is not part of this library).
+//       (router_scores_topk_normalize_kernel).
+//   kimi_k2_router_noaux_tc_cuda   the logits GEMM (hidden x gate^T, fp32
+//       out, kimi_router.cu:108-142, cuBLAS there, dense.hip's MFMA GEMM
+//       here) followed by the select stage above, with the reference's
+//       guards (kimi_router.cu:148-187).
 //   pega_dsv2_router_select   softmax (max-subtracted, sequential sum,
 //       divide), top-k by probability (ties -> lower id), then ordered by
 //       expert id; weight = probability.
@@ -14,6 +17,7 @@
 // Scores use e^x rounded from a double-precision exp, so that the CPU checker
 // reproduces them bit for bit and the selected indices agree exactly.
 #include "common.h"
+#include "pega_moe.h"
 
 namespace pega {
 namespace {
@@ -257,4 +261,34 @@ PEGA_API int pega_dsv2_router_select(const float* logits, float* topk_weight, in
   launch_slots<Dsv2Launch>(n_experts, dim3(grid), stream, logits, topk_weight, topk_idx, tokens,
                            n_experts, topk);
   return launch_status("dsv2_router_select");
+}
+
+// Reference: pegainfer-kernels/src/ffi/kimi.rs:52-66 (kimi_k2_router_noaux_tc_cuda,
+// csrc/kimi_k2/kimi_router.cu:148-187): logits[padded_tokens][n_experts] =
+// hidden[padded_tokens][hidden_dim] . gate_weight[n_experts][hidden_dim]^T in fp32
+// (CUBLAS_COMPUTE_32F_PEDANTIC there: no reduced-precision accumulation; here fp32 MFMA
+// accumulation, summed over K shares in a fixed order), then the select stage over the
+// active tokens.  Same rejections as the reference (1 for null pointers, token counts,
+// n_experts != 384, topk != 8, route_scale <= 0); additionally 801 when hidden_dim % 32 != 0
+// or hidden / gate_weight are not 16-byte aligned (the MFMA GEMM's layout; Kimi-K2's
+// hidden_dim is 7168).
+PEGA_API int kimi_k2_router_noaux_tc_cuda(const uint16_t* hidden, const uint16_t* gate_weight,
+                                          const float* e_score_correction_bias, float* logits,
+                                          float* topk_weight, int32_t* topk_idx,
+                                          int active_tokens, int padded_tokens, int hidden_dim,
+                                          int n_experts, int topk, float route_scale,
+                                          hipStream_t stream) {
+  if (!hidden || !gate_weight || !e_score_correction_bias || !logits || !topk_weight || !topk_idx)
+    return fail(kInvalidValue, "kimi_k2_router_noaux_tc: null pointer");
+  if (active_tokens <= 0 || padded_tokens <= 0 || active_tokens > padded_tokens ||
+      hidden_dim <= 0 || n_experts <= 0 || topk <= 0 || topk > n_experts || n_experts != 384 ||
+      topk != 8 || !(route_scale > 0.0f))
+    return fail(kInvalidValue,
+                "kimi_k2_router_noaux_tc: bad shape active=%d padded=%d hidden=%d experts=%d "
+                "topk=%d", active_tokens, padded_tokens, hidden_dim, n_experts, topk);
+  const int rc = dense_gemm_f32(gate_weight, hidden, logits, n_experts, padded_tokens, hidden_dim,
+                                stream, "kimi_k2_router_noaux_tc (logits)");
+  if (rc != kSuccess) return rc;
+  return pega_kimi_router_select(logits, e_score_correction_bias, topk_weight, topk_idx,
+                                 active_tokens, n_experts, topk, route_scale, stream);
 }

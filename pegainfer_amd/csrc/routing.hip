@@ -21,6 +21,7 @@
 // count launch and a scatter launch with one workgroup per expert produce the
 // same bytes (the wide path below).
 #include "common.h"
+#include "pega_moe.h"
 
 namespace pega {
 namespace {
@@ -450,12 +451,16 @@ PEGA_API int pega_moe_align_block_size(const int32_t* topk_idx, int32_t* sorted_
                                 max_m_blocks, stream);
 }
 
-// Reference: pegainfer-kernels/src/ffi/kimi.rs:296-307; kimi_experts.cu:435-459
-// (which limits num_local_experts to 64; this one allows up to 1024).
+// Reference: pegainfer-kernels/src/ffi/kimi.rs:296-307; kimi_experts.cu:435-459,
+// including its rejection of more than 64 local experts (:446, status 1).
 PEGA_API int kimi_deepep_build_marlin_routing_on_stream(
     const int32_t* psum_expert, int32_t* sorted_token_ids, int32_t* expert_ids,
     int32_t* num_tokens_post_padded, int num_local_experts, int alignment, int block_size,
     int max_padded_tokens, int max_m_blocks, hipStream_t stream) {
+  if (num_local_experts > 64)
+    return pega::fail(pega::kInvalidValue,
+                      "kimi deepep_build_routing: at most 64 local experts (got %d)",
+                      num_local_experts);
   return pega::deepep_build_routing(psum_expert, sorted_token_ids, expert_ids,
                                     num_tokens_post_padded, num_local_experts, alignment,
                                     block_size, max_padded_tokens, max_m_blocks, stream);

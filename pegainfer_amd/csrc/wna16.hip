@@ -26,6 +26,8 @@
 // A[m][32g + 16h + {0..3, 8..11}] (X1/Y1) and {4..7, 12..15} (X2/Y2), i.e.
 // one 32-byte read.  Scales of n0 and n1 are adjacent in the permuted scale
 // row: index 8*(c%8) + 2*(c/8) (+1).
+#include <algorithm>
+
 #include "common.h"
 #include "pega_moe.h"
 
@@ -912,9 +914,12 @@ int wna16_gemm(const uint16_t* input, uint16_t* output, float* c_tmp, long long 
   if (!valid_block_size(moe_block_size))
     return fail(kInvalidValue, "wna16_gemm: moe_block_size %d not in {8,16,32,48,64}",
                 moe_block_size);
-  if (size_k % 64 != 0 || size_n % 64 != 0)
-    return fail(kNotSupported, "wna16_gemm: size_k %% 64 and size_n %% 64 must be 0 (k=%d n=%d)",
+  if (size_k % 32 != 0 || size_n % 64 != 0)
+    return fail(kInvalidValue, "wna16_gemm: size_k %% 32 and size_n %% 64 must be 0 (k=%d n=%d)",
                 size_k, size_n);
+  if (moe_block_size > 16 && size_k % 64 != 0)
+    return fail(kNotSupported, "wna16_gemm: the prefill tile kernel needs size_k %% 64 == 0 "
+                "(k=%d)", size_k);
   if ((reinterpret_cast<uintptr_t>(input) & 15u) != 0 ||
       (reinterpret_cast<uintptr_t>(output) & 15u) != 0)
     return fail(kInvalidValue, "wna16_gemm: input and output must be 16-byte aligned");
@@ -979,8 +984,10 @@ int wna16_w13_swiglu(const uint16_t* input, uint16_t* act, float* partials, long
     return fail(kInvalidValue, "w13_swiglu: block size %d not in {8, 16, 32, 48, 64}",
                 moe_block_size);
   const int size_n = 2 * inter;
-  if (size_k % 64 != 0 || inter % 64 != 0)
-    return fail(kNotSupported, "w13_swiglu: size_k %% 64 and inter %% 64 must be 0");
+  if (size_k % 32 != 0 || inter % 64 != 0)
+    return fail(kInvalidValue, "w13_swiglu: size_k %% 32 and inter %% 64 must be 0");
+  if (moe_block_size > 16 && size_k % 64 != 0)
+    return fail(kNotSupported, "w13_swiglu: the prefill tile kernel needs size_k %% 64 == 0");
   if ((reinterpret_cast<uintptr_t>(input) & 15u) != 0 ||
       (reinterpret_cast<uintptr_t>(act) & 15u) != 0 ||
       (reinterpret_cast<uintptr_t>(partials) & 15u) != 0)
@@ -1139,12 +1146,34 @@ PEGA_API int kimi_marlin_wna16_gemm_cuda(
     int workspace_len, int sorted_token_ids_len, int moe_block_size, int top_k,
     bool mul_topk_weights, int size_m, int size_n, int size_k, int local_experts, int group_size,
     int sm_count, hipStream_t stream) {
-  if (!workspace || !c_tmp)
-    return pega::fail(pega::kInvalidValue, "kimi wna16_gemm: workspace and c_tmp are required");
-  if (local_experts != 48)
-    return pega::fail(pega::kInvalidValue, "kimi wna16_gemm: local_experts must be 48");
+  // the reference's checks, in its order (kimi_marlin_wna16.cu:264-309)
+  if (!input || !output || !b_qweight || !b_scales || !workspace || !sorted_token_ids ||
+      !expert_ids || !num_tokens_post_padded || !topk_weights)
+    return pega::fail(pega::kInvalidValue, "kimi wna16_gemm: null pointer");
+  if (!c_tmp) return pega::fail(pega::kInvalidValue, "kimi wna16_gemm: c_tmp is required");
+  if (local_experts != 48 || group_size != 32 || top_k <= 0 || size_m <= 0 || size_n <= 0 ||
+      size_k <= 0 || sorted_token_ids_len <= 0)
+    return pega::fail(pega::kInvalidValue,
+                      "kimi wna16_gemm: bad shape (experts=%d group=%d topk=%d m=%d n=%d k=%d)",
+                      local_experts, group_size, top_k, size_m, size_n, size_k);
+  if (!pega::valid_block_size(moe_block_size))
+    return pega::fail(pega::kInvalidValue, "kimi wna16_gemm: moe_block_size %d not in "
+                      "{8,16,32,48,64}", moe_block_size);
   if (size_k % 16 != 0 || size_n % 64 != 0 || size_k % group_size != 0)
-    return pega::fail(pega::kInvalidValue, "kimi wna16_gemm: bad k/n");
+    return pega::fail(pega::kInvalidValue, "kimi wna16_gemm: bad k/n (k=%d n=%d)", size_k,
+                      size_n);
+  // the lock-workspace floor (:305-309), sm_count <= 0 meaning the device's CU count; the
+  // locks are not used here, but a caller that sized them too small is rejected the same way
+  int cus = sm_count;
+  if (cus <= 0) cus = pega::current_cu_count();
+  if (cus <= 0) return pega::fail(pega::kInvalidValue, "kimi wna16_gemm: no device");
+  const long long min_ws = std::min(static_cast<long long>(size_n / 64) *
+                                        (sorted_token_ids_len / moe_block_size),
+                                    4LL * cus);
+  if (workspace_len < min_ws)
+    return pega::fail(pega::kInvalidValue,
+                      "kimi wna16_gemm: workspace_len %d below min(n_tiles * m_blocks, 4 * "
+                      "sm_count) = %lld", workspace_len, min_ws);
   const long long c_tmp_len = static_cast<long long>(size_n) * sorted_token_ids_len *
                               (moe_block_size == 8 ? 2 : 1);
   return pega::wna16_gemm(input, output, c_tmp, c_tmp_len, b_qweight, b_scales, workspace,

@@ -267,7 +267,9 @@ class ExpertFFN:
 class Dsv2MoeLayer:
     """DeepSeek-V2-Lite-shaped MoE: softmax top-k routed experts (weights applied
     in the fp32 combine, route order = expert id) plus a shared expert, joined
-    as bf16(routed_f32 + shared) (kimi_add_f32_bf16_to_bf16 rounding)."""
+    as the reference rounds it: bf16(f(bf16(routed_f32)) + f(shared))
+    (f32_to_bf16 at nccl_backend.rs:544-545, then the bf16 add at
+    runtime/moe.rs:656)."""
 
     def __init__(self, routed: RoutedExperts, shared: ExpertFFN, device="cuda",
                  overlap_shared: bool = True):
@@ -300,7 +302,7 @@ class Dsv2MoeLayer:
                                    self.routed.topk)
             self.routed.forward(hidden, self.topk_idx[:T], self.topk_w[:T], self.routed_f32[:T],
                                 combine="weighted", companion=companion)
-            ops.kimi_add_f32_bf16_to_bf16(self.routed_f32[:T], self.shared_out[:T], out)
+            ops.moe_join_routed_shared(self.routed_f32[:T], self.shared_out[:T], out)
             return out
         main = torch.cuda.current_stream()
         if self.overlap_shared and self.side is None:
@@ -316,7 +318,7 @@ class Dsv2MoeLayer:
             main.wait_stream(self.side)
         else:
             self.shared.forward(hidden, self.shared_out[:T])
-        ops.kimi_add_f32_bf16_to_bf16(self.routed_f32[:T], self.shared_out[:T], out)
+        ops.moe_join_routed_shared(self.routed_f32[:T], self.shared_out[:T], out)
         return out
 
 

@@ -481,6 +481,27 @@ def wna16_prefill_pair(first: "_lib.Wna16Problem", second: "_lib.Wna16Problem") 
     _lib.call("pega_wna16_prefill_pair", ctypes.byref(first), ctypes.byref(second), _stream())
 
 
+def kimi_marlin_wna16_expanded_w13_gemm(workspace, routing, input, weight, topk_weight,
+                                        output_w13):
+    """W13 over the DeepEP expanded (expert-major) buffer: top_k = 1, no weight
+    multiply, size_m = the expanded capacity (experts.rs:1328-1360).  `routing` comes
+    from kimi_deepep_build_marlin_routing_on_stream: identity ids for real rows, the
+    capacity sentinel for pad rows, read on device up to num_tokens_post_padded."""
+    _ensure(topk_weight.numel() >= routing.route_elems,
+            f"topk_weight len must cover {routing.route_elems}, got {topk_weight.numel()}")
+    wna16_gemm(workspace, routing, input, weight, topk_weight, output_w13, top_k=1,
+               mul_topk_weights=False, size_m=routing.active_tokens)
+
+
+def kimi_marlin_wna16_expanded_w2_gemm(workspace, routing, input, weight, topk_weight, output):
+    """W2 over the DeepEP expanded buffer: top_k = 1, one bf16 top-k weight per
+    expert-major row, size_m = route_elems (experts.rs:1364-1401)."""
+    _ensure(topk_weight.numel() >= routing.route_elems,
+            f"topk_weight len must cover {routing.route_elems}, got {topk_weight.numel()}")
+    wna16_gemm(workspace, routing, input, weight, topk_weight, output, top_k=1,
+               mul_topk_weights=True, size_m=routing.route_elems)
+
+
 def kimi_marlin_wna16_w13_gemm(workspace, routing, input, weight, topk_weight, output_w13):
     """W13 call: top_k = routing.topk, no weight multiply, size_m = active tokens
     (experts.rs:1024-1080)."""
@@ -564,6 +585,35 @@ def kimi_add_f32_bf16_to_bf16(a, b, out) -> None:
     _lib.call("kimi_add_f32_bf16_to_bf16_cuda", _ptr(a), _ptr(b), _ptr(out), n, _stream())
 
 
+def f32_to_bf16(x: torch.Tensor, out: torch.Tensor) -> None:
+    """out = bf16(x) (f32_to_bf16_hidden_into, pegainfer-kernels/src/ops/elementwise.rs:579-603)."""
+    n = out.numel()
+    _ensure(x.dtype == torch.float32 and x.numel() >= n,
+            f"f32 input len {x.numel()} < bf16 output len {n}")
+    _ensure(_is_bf16(out), "f32_to_bf16 output must be bf16")
+    _lib.call("f32_to_bf16_cuda", _ptr(x), _ptr(out), n, _stream())
+
+
+def add_bf16(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor) -> None:
+    """out = bf16(a + b) over bf16 tensors (add_batch_into, elementwise.rs:14-40)."""
+    _ensure(a.numel() == b.numel() == out.numel(), "add: shapes differ")
+    _ensure(_is_bf16(a) and _is_bf16(b) and _is_bf16(out), "add operands must be bf16")
+    _lib.call("add_cuda", _ptr(a), _ptr(b), _ptr(out), out.numel(), _stream())
+
+
+def moe_join_routed_shared(routed_f32: torch.Tensor, shared: torch.Tensor,
+                           out: torch.Tensor) -> None:
+    """DeepSeek-V2-Lite routed + shared join, rounded as the reference does it:
+    out = bf16(f(bf16(routed)) + f(shared)) (nccl_backend.rs:544-545 then
+    runtime/moe.rs:656), in one launch."""
+    n = out.numel()
+    _ensure(routed_f32.dtype == torch.float32 and routed_f32.numel() >= n, "routed too small")
+    _ensure(shared.numel() == n and _is_bf16(shared) and _is_bf16(out),
+            "shared / out must be bf16 of the same size")
+    _lib.call("pega_moe_join_routed_shared_bf16", _ptr(routed_f32), _ptr(shared), _ptr(out), n,
+              _stream())
+
+
 # --------------------------------------------------------------------------
 # Dense bf16 GEMM (the shared expert's projections)
 # --------------------------------------------------------------------------
@@ -610,6 +660,28 @@ def kimi_router_select(logits: torch.Tensor, bias: torch.Tensor, topk_weight: to
     _ensure(logits.dtype == torch.float32 and bias.dtype == torch.float32, "logits/bias f32")
     _lib.call("pega_kimi_router_select", _ptr(logits), _ptr(bias), _ptr(topk_weight),
               _ptr(topk_idx), active_tokens, n_experts, topk, float(route_scale), _stream())
+
+
+def kimi_k2_router_noaux_tc(hidden: torch.Tensor, gate_weight: torch.Tensor,
+                            e_score_correction_bias: torch.Tensor, logits: torch.Tensor,
+                            topk_weight: torch.Tensor, topk_idx: torch.Tensor, active_tokens: int,
+                            padded_tokens: int, route_scale: float = 1.0) -> None:
+    """The Kimi router in one call (router.rs:182-229 -> kimi_k2_router_noaux_tc_cuda):
+    fp32 logits [padded_tokens, 384] = hidden . gate^T, then sigmoid top-8 of
+    score + bias with renormalised weights for the first active_tokens rows."""
+    n_experts, hidden_dim = gate_weight.shape
+    _ensure(_is_bf16(hidden) and _is_bf16(gate_weight), "hidden / gate_weight must be bf16")
+    _ensure(hidden.numel() >= padded_tokens * hidden_dim, "hidden must cover padded_tokens rows")
+    _ensure(logits.dtype == torch.float32 and logits.numel() >= padded_tokens * n_experts,
+            "logits must be f32 [padded_tokens, n_experts]")
+    _ensure(e_score_correction_bias.dtype == torch.float32 and
+            e_score_correction_bias.numel() >= n_experts, "bias must be f32 [n_experts]")
+    _ensure(topk_weight.numel() >= active_tokens * KIMI_K2_TOPK and
+            topk_idx.numel() >= active_tokens * KIMI_K2_TOPK, "top-k outputs too small")
+    _lib.call("kimi_k2_router_noaux_tc_cuda", _ptr(hidden), _ptr(gate_weight),
+              _ptr(e_score_correction_bias), _ptr(logits), _ptr(topk_weight), _ptr(topk_idx),
+              active_tokens, padded_tokens, hidden_dim, n_experts, KIMI_K2_TOPK,
+              float(route_scale), _stream())
 
 
 def dsv2_router_select(logits: torch.Tensor, topk_weight: torch.Tensor, topk_idx: torch.Tensor,

@@ -104,3 +104,26 @@ C4 = Config("c4_dsv2lite_moe_prefill_t512", 4, 2048, 1408, 64, 6, 512,
 C5 = Config("c5_kimi_prefill_t4096_zipf", 5, 7168, 2048, 48, 8, 4096,
             "Kimi-K2 local-expert prefill, 4096 tokens, Zipf(1.2) local routes")
 CONFIGS = {c.name: c for c in (C1, C2, C3, C4, C5)}
+
+
+def kimi_topk_margin(logits: np.ndarray, bias, topk: int = 8) -> np.ndarray:
+    """Per token, the smallest gap between neighbours among the top topk + 1 of
+    sigmoid(logit) + bias (fp64).  The Kimi router keeps its picks in selection
+    order, so every neighbouring pair up to the first unpicked one decides the
+    output; a gap well above a few fp32 ulps (1e-6) means exp implementations that
+    differ by an ulp still pick the same indices in the same order."""
+    s = 1.0 / (1.0 + np.exp(-np.asarray(logits, np.float64)))
+    c = s + np.asarray(bias, np.float64)
+    top = -np.sort(-c, axis=1)[:, :topk + 1]
+    return (top[:, :-1] - top[:, 1:]).min(axis=1)
+
+
+def dsv2_topk_margin(logits: np.ndarray, topk: int = 6) -> np.ndarray:
+    """Per token, the gap between the topk-th and the next softmax probability
+    (fp64).  The DeepSeek-V2-Lite router sorts its picks by expert id, so only this
+    boundary decides the output."""
+    l = np.asarray(logits, np.float64)
+    p = np.exp(l - l.max(axis=1, keepdims=True))
+    p /= p.sum(axis=1, keepdims=True)
+    top = -np.sort(-p, axis=1)
+    return top[:, topk - 1] - top[:, topk]

@@ -141,3 +141,50 @@ def test_dense_w13_swiglu_rejects():
     assert L.pega_dense_w13_swiglu(p, p, p, 16, 4, 48, s) == 801   # K % 32
     assert L.pega_dense_w13_swiglu(None, p, p, 16, 4, 64, s) == 1
     torch.cuda.synchronize()
+
+
+def _token_blocks(M, N, swiglu, cu):
+    """The launcher's (workgroup rows, token blocks) choice, restated so that the
+    shapes below provably reach the 3- and 4-token-block kernels (dense.hip)."""
+    mr = 2 if swiglu else (2 if M % 32 == 0 else 1)
+    gx = M // 16 if swiglu else M // (16 * mr)
+    rb = 1 if N <= 16 else 2 if N <= 32 else 3 if N <= 48 else 4
+    if rb > 1 and gx * -(-N // (16 * rb)) < cu:
+        rb = (rb + 1) // 2
+    return rb
+
+
+@pytest.mark.parametrize("M,N,K,rb", [(7168, 256, 2048, 4), (8192, 40, 1024, 3),
+                                      (4096, 100, 7168, 4), (8192, 48, 512, 3)])
+def test_dense_gemm_three_and_four_token_blocks(oracle, M, N, K, rb):
+    """Prefill-sized shared-expert shapes whose launches use 3 or 4 token blocks per
+    workgroup (the D = 3 load ring and the larger reduction buffer)."""
+    cu = torch.cuda.get_device_properties(0).multi_processor_count
+    assert _token_blocks(M, N, False, cu) == rb
+    g = np.random.default_rng(M + N + K)
+    w = oracle.f32_to_bf16((g.standard_normal((M, K)) * 0.02).astype(np.float32))
+    x = oracle.f32_to_bf16(g.standard_normal((N, K)).astype(np.float32))
+    assert_bf16_close(_gemm(w, x), oracle.dense_gemm(w, x), what=f"dense {M}x{N}x{K} rb={rb}")
+    # exact operands: bit for bit
+    we = oracle.f32_to_bf16(np.ldexp(g.integers(-8, 8, (M, K)), g.integers(-4, 0, (M, K)))
+                            .astype(np.float32))
+    xe = oracle.f32_to_bf16(g.integers(-3, 4, (N, K)).astype(np.float32))
+    ref = oracle.bf16_to_f32(xe).astype(np.float32) @ oracle.bf16_to_f32(we).astype(np.float32).T
+    assert np.array_equal(_gemm(we, xe), oracle.f32_to_bf16(ref))
+
+
+@pytest.mark.parametrize("I,N,K,rb", [(2048, 256, 7168, 4), (4096, 40, 1024, 3)])
+def test_dense_w13_swiglu_three_and_four_token_blocks(oracle, I, N, K, rb):
+    from pegainfer_amd import ops
+    cu = torch.cuda.get_device_properties(0).multi_processor_count
+    assert _token_blocks(I, N, True, cu) == rb
+    g = np.random.default_rng(I + N + K)
+    w = dev(oracle.f32_to_bf16((g.standard_normal((2 * I, K)) * 0.02).astype(np.float32)))
+    x = dev(oracle.f32_to_bf16(g.standard_normal((N, K)).astype(np.float32)))
+    gu = torch.zeros(N, 2 * I, dtype=torch.bfloat16, device="cuda")
+    ops.gemm_graphsafe(w, x, gu)
+    chain = torch.zeros(N, I, dtype=torch.bfloat16, device="cuda")
+    ops.kimi_marlin_w13_swiglu(gu, chain, N, I)
+    fused = torch.full((N, I), float("nan"), dtype=torch.bfloat16, device="cuda")
+    ops.dense_w13_swiglu(w, x, fused)
+    assert np.array_equal(host(fused), host(chain))

@@ -110,3 +110,27 @@ def test_residual_joins_bit_exact(oracle):
     assert np.array_equal(host(out), oracle.residual_add_scaled_bf16(h, p, rb, 2.827))
     ops.kimi_add_f32_bf16_to_bf16(dev(rf), dev(h), out)
     assert np.array_equal(host(out), oracle.add_f32_bf16(rf, h))
+
+
+def test_f32_to_bf16_add_and_dsv2_join_bit_exact(oracle):
+    """f32_to_bf16_cuda and add_cuda (the reference symbols) and the fused DeepSeek-V2-Lite
+    join pega_moe_join_routed_shared_bf16, against the oracle's two-rounding join; the
+    planted pairs are ones where a single rounding of routed + shared differs."""
+    from pegainfer_amd import ops
+    g = np.random.default_rng(31)
+    for n in (512 * 2048, 1000, 7):  # vector path, then element tails / scalar path
+        r = (g.standard_normal(n) * 3).astype(np.float32)
+        r[:2] = [1.0 + 2 ** -8 + 2 ** -12, 1.0 + 2 ** -9]
+        sh = _bf16_rand(g, n)
+        sh[:2] = oracle.f32_to_bf16(np.array([2 ** -8, 2 ** -9], np.float32))
+        rb = torch.zeros(n, dtype=torch.bfloat16, device="cuda")
+        ops.f32_to_bf16(dev(r), rb)
+        assert np.array_equal(host(rb), oracle.f32_to_bf16_n(r))
+        out = torch.zeros(n, dtype=torch.bfloat16, device="cuda")
+        ops.add_bf16(rb, dev(sh), out)
+        want = oracle.dsv2_join(r, sh)
+        assert np.array_equal(host(out), want)
+        fused = torch.full((n,), 5.0, dtype=torch.bfloat16, device="cuda")
+        ops.moe_join_routed_shared(dev(r), dev(sh), fused)
+        assert np.array_equal(host(fused), want)
+        assert want[0] != oracle.add_f32_bf16(r[:1], sh[:1])[0]

@@ -352,3 +352,19 @@ def test_prefill_pair_matches_single_launches(oracle, first, second):
         assert (ref != 0x40A0).any()
         if spec["E"] > 1:
             assert (ref == 0x40A0).all(axis=1).any(), "rows of other GPUs' routes keep bf16(5.0)"
+
+
+@pytest.mark.parametrize("bs,K", [(8, 2080), (16, 1056)])
+def test_gemm_decode_accepts_k_multiple_of_32(oracle, bs, K):
+    """The reference accepts any K that is a multiple of 16 and of the group size 32
+    (kimi_marlin_wna16.cu:284-286); the decode kernels work in 32-k groups, so an odd
+    group count (K % 64 == 32) runs and matches the oracle bit for bit on exact data."""
+    g = np.random.default_rng(K)
+    E, N, T = 48, 128, 6
+    q = g.integers(-8, 8, size=(E, N, K))
+    scale_bits = oracle.f32_to_bf16(np.ldexp(1.0, g.integers(-4, 1, size=(E, N, K // 32))).astype(np.float32))
+    a_bits = oracle.f32_to_bf16(g.integers(-3, 4, size=(T, K)).astype(np.float32))
+    idx = g.integers(0, 96, size=(T, 8))
+    got, ref = _run(oracle, E=E, N=N, K=K, T=T, topk=8, bs=bs, mul=False, a_bits=a_bits, q=q,
+                    scale_bits=scale_bits, idx=idx, tw=np.ones((T, 8), np.float32))
+    assert np.array_equal(got, ref)

@@ -107,6 +107,9 @@ def test_c3_kimi_decode_layer(oracle):
     hidden = synth.normal_bf16(synth.rng(3, 2), (T, H))
     logits = synth.rng(3, 3).standard_normal((T, 384), dtype=np.float32)
     bias = np.zeros(384, np.float32)
+    # neighbouring score + bias values among each token's top 9 differ by far more than
+    # an ulp: the picks and their order do not depend on the exp implementation
+    assert synth.kimi_topk_margin(logits, bias).min() > 1e-6
     bs = ops.kimi_marlin_block_size(T)
     assert bs == 16
     moe = _routed_layer(gate, up, down, tokens=T, topk=8, block_size=bs)
@@ -163,6 +166,9 @@ def test_c4_dsv2_layer(oracle):
                   synth.int4_checkpoint(g, 1, H, 2 * I))
     hidden = synth.normal_bf16(synth.rng(4, 2), (T, H))
     logits = synth.rng(4, 3).standard_normal((T, E), dtype=np.float32)
+    # every token's 6th/7th probability gap is far above an ulp: the selected set does
+    # not depend on the exp implementation
+    assert synth.dsv2_topk_margin(logits, topk).min() > 1e-6
     bs = ops.kimi_marlin_block_size(T, topk=topk, local_experts=E)
     routed = _routed_layer(gate, up, down, tokens=T, topk=topk, block_size=bs)
     shared = layer.ExpertFFN(layer.package_w13(sg, su), layer.package_projection(*sd), max_rows=T)
@@ -190,7 +196,8 @@ def test_c4_dsv2_layer(oracle):
     routed_f32 = host(moe.routed_f32)
     assert np.array_equal(routed_f32, oracle.weighted_topk_sum(ro, ref_w, T, topk, H))
     sh = host(moe.shared_out)
-    assert np.array_equal(host(out), oracle.add_f32_bf16(routed_f32, sh))
+    # the join as the reference rounds it: bf16(f(bf16(routed)) + f(shared))
+    assert np.array_equal(host(out), oracle.dsv2_join(routed_f32, sh))
     # the shared expert: one INT4 expert over all tokens (W13 + SwiGLU fused, then W2)
     sI = 2 * I
     sbs = shared.up.block_size
@@ -267,3 +274,72 @@ def test_c5_kimi_prefill_sampled(oracle):
     assert np.array_equal(act[local], oracle.swiglu(g13[local], I))
     assert (np.abs((ro[local].astype(np.uint32) << 16).view(np.float32)).sum(axis=1) > 0).all()
     assert np.array_equal(host(out), oracle.sum_topk_rows(ro, T, 8, H))
+
+
+def _exact_int4(g, E, N, K):
+    """Checkpoint tensors whose dequantised weights are q * 2^e, e in {-2, -1, 0}: with
+    small-integer activations every product and partial sum of a K <= 7168 dot product
+    is an exact fp32 number (magnitudes below 2^18 on a 2^-2 grid), so any summation
+    order gives the same fp32 sum and a float32 BLAS product reproduces it exactly."""
+    from oracle import oracle
+    q = g.integers(-8, 8, size=(E, N, K), dtype=np.int8)
+    exps = g.integers(-2, 1, size=(E, N, K // 32))
+    scales_f = np.ldexp(np.float32(1.0), exps).astype(np.float32)
+    u = (q + 8).astype(np.uint8)
+    packed = (u[..., 0::2] | (u[..., 1::2] << 4)).astype(np.uint8)
+    return (packed, oracle.f32_to_bf16(scales_f)), q, scales_f
+
+
+def _exact_rows(a_f32, q_e, s_e):
+    """fp32 [rows, N] = a . (q * s)^T, exact for the inputs of _exact_int4."""
+    w = (q_e.astype(np.float32) * np.repeat(s_e, 32, axis=1)).astype(np.float32)
+    return a_f32 @ w.T
+
+
+def test_c5_every_block_exact_inputs(oracle):
+    """C5's routing at full size (4096 tokens, 6565 Zipf routes, every m-block of all 48
+    experts) with exact inputs: every routed row of W13 must equal the float32 product
+    rounded to bf16 bit for bit, the fused SwiGLU must be SwiGLU of those bits, and every
+    routed W2 row (exact activations fed in, bf16 top-k weight applied) likewise."""
+    from pegainfer_amd import ops, synth
+    E, H, I, T = 48, 7168, 2048, 4096
+    g = np.random.default_rng(0x5EED0005)
+    (gp, gs), qg, sg = _exact_int4(g, E, I, H)
+    (upk, us), qu, su = _exact_int4(g, E, I, H)
+    (dp, ds), qd, sd = _exact_int4(g, E, H, I)
+    a = g.integers(-2, 3, size=(T, H)).astype(np.float32)
+    idx, w = synth.zipf_local_topk(synth.rng(5, 3), T)
+    bs = ops.kimi_marlin_block_size(T)
+    moe = _routed_layer((gp, gs), (upk, us), (dp, ds), tokens=T, topk=8, block_size=bs)
+    out = torch.zeros(T, H, dtype=torch.float32, device="cuda")
+    a_bits = oracle.f32_to_bf16(a)
+    hidden_d, w_d, idx_d = dev(a_bits), dev(w), dev(idx)
+    moe.forward(hidden_d, idx_d, w_d, out)
+    g13 = _unfused_w13(moe, hidden_d, w_d, T)
+    act = host(moe.act[:T * 8])
+    flat = idx.reshape(-1)
+    local = flat < E
+    routing = _routing_host(moe.routing)
+    nblocks = int(routing["num_tokens_post_padded"][0]) // bs
+    assert nblocks > 100 and np.unique(routing["expert_ids"][:nblocks]).size == E
+    qw13 = np.concatenate([qg, qu], axis=1)
+    sw13 = np.concatenate([sg, su], axis=1)
+    for e in range(E):
+        rows = np.flatnonzero(flat == e)
+        want = oracle.f32_to_bf16(_exact_rows(a[rows // 8], qw13[e], sw13[e]))
+        assert np.array_equal(g13[rows], want), f"W13 expert {e}"
+    assert np.array_equal(act[local], oracle.swiglu(g13[local], I))
+    # W2 over every routed row, with exact activations
+    act_x = np.zeros((T * 8, I), np.float32)
+    act_x[local] = g.integers(-3, 4, size=(int(local.sum()), I))
+    ro = torch.zeros(T * 8, H, dtype=torch.bfloat16, device="cuda")
+    ops.wna16_gemm(moe.gemm_ws, moe.routing, dev(oracle.f32_to_bf16(act_x)), moe.w2, w_d, ro,
+                   top_k=1, mul_topk_weights=True, size_m=T * 8)
+    ro = host(ro)
+    twb = oracle.bf16_to_f32(oracle.f32_to_bf16(w.reshape(-1)))
+    for e in range(E):
+        rows = np.flatnonzero(flat == e)
+        acc = oracle.f32_to_bf16(_exact_rows(act_x[rows], qd[e], sd[e]))
+        want = oracle.f32_to_bf16(oracle.bf16_to_f32(acc) * twb[rows][:, None])
+        assert np.array_equal(ro[rows], want), f"W2 expert {e}"
+    assert (ro[~local] == 0).all()

@@ -171,3 +171,38 @@ def test_kimi_router_select_expert_counts(oracle, n_experts, topk):
     ref_idx, ref_w = oracle.kimi_router(logits, bias, topk, 1.0)
     assert np.array_equal(host(idx), ref_idx)
     assert np.array_equal(host(w), ref_w)
+
+
+@pytest.mark.parametrize("active,padded,seed", [(64, 64, 0), (5, 64, 1), (1, 1, 2), (300, 320, 3)])
+def test_kimi_router_noaux_tc_symbol(oracle, active, padded, seed):
+    """kimi_k2_router_noaux_tc_cuda (ffi/kimi.rs:52-66): fp32 logits of every padded row
+    within the fp32-accumulation bound of the oracle's (an fp64-free bound: K roundings
+    of the running sum), then the select stage over the active rows bit for bit against
+    the oracle fed the GPU's own logits; rows past active_tokens are not written."""
+    from pegainfer_amd import ops, synth
+    g = np.random.default_rng(40 + seed)
+    H = 7168
+    hidden = synth.normal_bf16(g, (padded, H))
+    gate = synth.normal_bf16(g, (384, H), std=0.01)
+    bias = (g.standard_normal(384) * 0.01).astype(np.float32)
+    logits = torch.full((padded, 384), float("nan"), dtype=torch.float32, device="cuda")
+    w = torch.full((padded, 8), -1.0, dtype=torch.float32, device="cuda")
+    idx = torch.full((padded, 8), -5, dtype=torch.int32, device="cuda")
+    ops.kimi_k2_router_noaux_tc(dev(hidden), dev(gate), dev(bias), logits, w, idx, active, padded)
+    got_l = host(logits)
+    ref_l = oracle.dense_gemm_f32(gate, hidden)
+    hf = oracle.bf16_to_f32(hidden).astype(np.float64)
+    gf = oracle.bf16_to_f32(gate).astype(np.float64)
+    bound = 2 * H * 2.0 ** -24 * (np.abs(hf) @ np.abs(gf).T)  # both sums' rounding errors
+    assert np.isfinite(got_l).all()
+    assert (np.abs(got_l.astype(np.float64) - ref_l) <= bound).all()
+    ref_idx, ref_w = oracle.kimi_router(got_l[:active], bias, 8, 1.0)
+    assert np.array_equal(host(idx)[:active], ref_idx)
+    assert np.array_equal(host(w)[:active], ref_w)
+    assert (host(idx)[active:] == -5).all() and (host(w)[active:] == -1.0).all()
+    # the oracle's own logits pick the same experts where the margin is clear
+    m = synth.kimi_topk_margin(ref_l[:active], bias)
+    ok = m > 1e-4
+    assert ok.mean() > 0.9
+    ref_idx2, _ = oracle.kimi_router(ref_l[:active], bias, 8, 1.0)
+    assert np.array_equal(ref_idx2[ok], ref_idx[ok])

@@ -29,7 +29,8 @@ def test_header_declares_the_reference_entry_points():
                  "kimi_marlin_int4_reorder_scale_cuda", "kimi_marlin_int4_fuse_w13_cuda",
                  "kimi_residual_add_scaled_f32_cuda", "kimi_residual_add_scaled_bf16_cuda",
                  "kimi_add_f32_bf16_to_bf16_cuda", "kimi_deepep_build_marlin_routing_on_stream",
-                 "pegainfer_kernels_last_error"]:
+                 "kimi_k2_router_noaux_tc_cuda", "f32_to_bf16_cuda", "add_cuda", "gemm_cuda",
+                 "gemm_graphsafe_cuda", "pegainfer_kernels_last_error"]:
         assert name in syms, name
 
 
@@ -104,6 +105,95 @@ def test_gemm_rejects_reference_invalid_shapes():
     assert rc == 1  # the output rows are written with 16-byte stores
 
 
+def test_gemm_rejects_a_lock_workspace_below_the_reference_floor():
+    """kimi_marlin_wna16.cu:305-309: workspace_len < min(n_tiles * (sorted_len / bs),
+    4 * sm_count) is INVALID_VALUE, although the locks themselves are not used here."""
+    from pegainfer_amd import _lib
+    f = _lib.lib().kimi_marlin_wna16_gemm_cuda
+
+    def call(workspace_len, sm_count, sorted_len=1232, bs=16, n=4096):
+        rc = f(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, workspace_len,
+               sorted_len, bs, 8, False, 64, n, 7168, 48, 32, sm_count, NULL)
+        return rc, _lib.last_error()
+    # 64 column tiles x 77 m-blocks = 4928 > 4 * 256 = 1024: the floor is 1024
+    rc, msg = call(1023, 256)
+    assert rc == 1 and "workspace_len" in msg
+    # 4 * 78 = 312 with the reference's H20 SM count
+    rc, msg = call(311, 78)
+    assert rc == 1 and "workspace_len" in msg
+    # a tiny problem: 1 m-block x 1 column tile = 1 lock
+    rc, msg = call(0, 256, sorted_len=16, n=64)
+    assert rc == 1 and "workspace_len" in msg
+    # at the floor the check passes (the call then fails only for want of a device)
+    rc, msg = call(1024, 256)
+    assert "workspace_len" not in msg
+    # K % 16 == 0 but K % 32 != 0: the group size does not divide K
+    rc = f(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4096, 1232, 16, 8, False,
+           64, 4096, 7168 + 16, 48, 32, 256, NULL)
+    assert rc == 1
+
+
+def test_deepep_routing_rejects_more_than_64_experts_like_the_reference():
+    """kimi_experts.cu:446: num_local_experts > kRoutingBuilderMaxExperts (64) -> 1."""
+    rc, msg = _call("kimi_deepep_build_marlin_routing_on_stream", FAKE, FAKE, FAKE, FAKE, 65, 8,
+                    8, 1000, 125, NULL)
+    assert rc == 1 and "64" in msg
+
+
+def test_router_noaux_tc_rejects_like_the_reference():
+    """kimi_router.cu:162-171: null pointers, token counts, n_experts != 384, topk != 8,
+    route_scale <= 0 -> INVALID_VALUE; the MFMA logits GEMM needs hidden_dim % 32 == 0
+    (801 otherwise)."""
+    def call(active=64, padded=64, hidden=7168, experts=384, topk=8, scale=1.0, ptrs=None):
+        p = ptrs if ptrs is not None else [FAKE] * 6
+        return _call("kimi_k2_router_noaux_tc_cuda", *p, active, padded, hidden, experts, topk,
+                     ctypes.c_float(scale), NULL)
+    assert call(experts=256)[0] == 1
+    assert call(topk=6)[0] == 1
+    assert call(active=65)[0] == 1          # active_tokens > padded_tokens
+    assert call(active=0)[0] == 1
+    assert call(padded=0, active=0)[0] == 1
+    assert call(hidden=0)[0] == 1
+    assert call(scale=0.0)[0] == 1
+    assert call(scale=float("nan"))[0] == 1
+    assert call(ptrs=[FAKE] * 5 + [NULL])[0] == 1
+    rc, msg = call(hidden=7168 + 16)
+    assert rc == 801 and "K" in msg
+
+
+def test_dense_gemm_w_size_is_not_limited_only_its_workgroup_span():
+    """A W larger than 2 GiB (the unsharded Kimi lm_head, 163840 x 7168 bf16) passes the
+    range checks: each workgroup addresses only its own 32 rows.  With the SwiGLU
+    epilogue a workgroup spans gate to up rows, so (I + 16) * K * 2 must stay below 2 GiB."""
+    rc, msg = _call("gemm_cuda", FAKE, FAKE, FAKE, 163840, 64, 7168, NULL)
+    assert "2 GiB" not in msg  # (on a host without a GPU it then fails for want of a device)
+    rc, msg = _call("gemm_graphsafe_cuda", FAKE, FAKE, FAKE, 163840, 64, 7168, NULL)
+    assert "2 GiB" not in msg
+    rc, msg = _call("pega_dense_w13_swiglu", FAKE, FAKE, FAKE, 150000, 64, 7168, NULL)
+    assert rc == 801 and "2 GiB" in msg
+    rc, msg = _call("gemm_cuda", FAKE, FAKE, FAKE, 4096, 200_000, 7168, NULL)  # X 2.87 GB
+    assert rc == 801 and "2 GiB" in msg
+
+
+def test_elementwise_reference_symbols_reject_bad_arguments():
+    assert _call("f32_to_bf16_cuda", NULL, FAKE, 8, NULL)[0] == 1
+    assert _call("f32_to_bf16_cuda", FAKE, FAKE, -1, NULL)[0] == 1
+    assert _call("f32_to_bf16_cuda", FAKE, FAKE, 0, NULL)[0] == 0
+    assert _call("add_cuda", FAKE, NULL, FAKE, 8, NULL)[0] == 1
+    assert _call("add_cuda", FAKE, FAKE, FAKE, 0, NULL)[0] == 0
+    assert _call("pega_moe_join_routed_shared_bf16", FAKE, FAKE, NULL, 8, NULL)[0] == 1
+    assert _call("pega_moe_join_routed_shared_bf16", FAKE, FAKE, FAKE, 0, NULL)[0] == 0
+
+
+def test_repack_reference_symbols_return_invalid_value_on_every_failure():
+    """kimi_marlin_int4.cu:190,220,254,262 map every failure (a launch failure included) to
+    CUDA_ERROR_INVALID_VALUE; shape failures are 1 as well."""
+    assert _call("kimi_marlin_int4_reorder_weight_cuda", FAKE, FAKE, 7168, 2048, 48, 16,
+                 NULL)[0] == 1
+    assert _call("kimi_marlin_int4_reorder_scale_cuda", NULL, FAKE, 7168, 2048, 48, 32,
+                 NULL)[0] == 1
+
+
 def test_gemm_entries_reject_shapes_past_the_32_bit_ranges():
     """One expert's weights are addressed through a 32-bit range (<= 4 GiB) and the
     activations through one of at most 2 GiB (offset 2^31 reads zeros for rows that
@@ -157,8 +247,9 @@ def test_fused_w13_swiglu_rejects_bad_arguments():
                      base["k"], base["experts"], base["group"], 0, NULL)
     assert call(bs=24)[0] == 1             # block sizes 8, 16, 32, 48, 64 only
     assert call(group=64)[0] == 1
-    assert call(inter=2000)[0] == 801      # width must be a multiple of 64
-    assert call(k=7160)[0] == 801          # K must be a multiple of 64
+    assert call(inter=2000)[0] == 1        # width must be a multiple of 64
+    assert call(k=7160)[0] == 1            # K must be a multiple of the group (32)
+    assert call(k=7168 + 32, bs=64)[0] == 801  # the prefill tile kernel stages 64 k at a time
     assert call(m=0)[0] == 1
     odd = ctypes.c_void_p(0x1008)
     rc = _call("pega_wna16_w13_swiglu", FAKE, odd, FAKE, ctypes.c_longlong(1 << 20), FAKE, FAKE,

@@ -447,3 +447,120 @@ def test_dense_gemm_within_fp32_bound_of_fp64(oracle):
     # one bf16 rounding of the result plus K fp32 roundings of the running sum
     bound = 2.0 ** -8 * np.abs(exact) + K * 2.0 ** -24 * (np.abs(xf) @ np.abs(wf).T)
     assert (np.abs(got - exact) <= bound).all()
+
+
+# ---------------------------------------------------------------- router logits GEMM (fp32 out)
+# kimi_router.cu:108-142: cublasGemmEx(..., CUDA_R_32F output, COMPUTE_32F_PEDANTIC)
+def test_dense_gemm_f32_exact_small_integers(oracle):
+    """Every partial sum exact -> any summation order gives these fp32 bits, which an
+    fp64 matrix product reproduces; no bf16 rounding of the output."""
+    g = np.random.default_rng(17)
+    M, N, K = 384, 5, 7168
+    w = oracle.f32_to_bf16(np.ldexp(g.integers(-8, 8, (M, K)), g.integers(-6, -2, (M, K)))
+                           .astype(np.float32))
+    x = oracle.f32_to_bf16(g.integers(-3, 4, (N, K)).astype(np.float32))
+    y = oracle.dense_gemm_f32(w, x)
+    ref = oracle.bf16_to_f32(x).astype(np.float64) @ oracle.bf16_to_f32(w).astype(np.float64).T
+    assert y.dtype == np.float32 and np.array_equal(y, ref.astype(np.float32))
+    # fp32 output is not bf16-rounded: some results need more than 8 significant bits
+    assert (oracle.bf16_to_f32(oracle.f32_to_bf16(y)) != y).any()
+
+
+def test_dense_gemm_f32_one_hot_rows_and_rounding_agrees_with_bf16_gemm(oracle):
+    g = np.random.default_rng(18)
+    M, K = 64, 96
+    w = oracle.f32_to_bf16(g.standard_normal((M, K)).astype(np.float32))
+    x = np.zeros((2, K), np.uint16)
+    x[0, 5] = 0x3F80
+    x[1, 90] = 0xBF80  # -1.0
+    y = oracle.dense_gemm_f32(w, x)
+    assert np.array_equal(y[0], oracle.bf16_to_f32(w[:, 5]))
+    assert np.array_equal(y[1], -oracle.bf16_to_f32(w[:, 90]))
+    xr = oracle.f32_to_bf16(g.standard_normal((7, K)).astype(np.float32))
+    # same k-ascending fp32 sum: the bf16 GEMM is exactly the rounded fp32 one
+    assert np.array_equal(oracle.f32_to_bf16(oracle.dense_gemm_f32(w, xr)),
+                          oracle.dense_gemm(w, xr))
+
+
+def test_dense_gemm_f32_within_fp32_bound_of_fp64(oracle):
+    g = np.random.default_rng(19)
+    M, N, K = 384, 4, 7168
+    w = oracle.f32_to_bf16((g.standard_normal((M, K)) * 0.02).astype(np.float32))
+    x = oracle.f32_to_bf16(g.standard_normal((N, K)).astype(np.float32))
+    wf, xf = oracle.bf16_to_f32(w).astype(np.float64), oracle.bf16_to_f32(x).astype(np.float64)
+    exact = xf @ wf.T
+    got = oracle.dense_gemm_f32(w, x).astype(np.float64)
+    bound = K * 2.0 ** -24 * (np.abs(xf) @ np.abs(wf).T)
+    assert (np.abs(got - exact) <= bound).all()
+
+
+# ---------------------------------------------------------------- DSV2 routed + shared join
+def test_f32_to_bf16_n_matches_numpy_rounding_and_ties(oracle):
+    g = np.random.default_rng(20)
+    x = np.concatenate([g.standard_normal(1000).astype(np.float32) * 100,
+                        np.array([1 + 2 ** -8, 1 + 3 * 2 ** -8, -0.0, 3e38], np.float32)])
+    got = oracle.f32_to_bf16_n(x)
+    # numpy: round half to even on the 16 dropped bits, computed independently in int64
+    u = x.view(np.uint32).astype(np.int64)
+    low, high = u & 0xFFFF, u >> 16
+    up = (low > 0x8000) | ((low == 0x8000) & (high & 1 == 1))
+    want = (high + up).astype(np.uint16)
+    assert np.array_equal(got, want)
+    assert got[-4] == 0x3F80 and got[-3] == 0x3F82 and got[-2] == 0x8000
+
+
+def test_add_bf16_is_float32_add_then_rounding(oracle):
+    g = np.random.default_rng(21)
+    a = oracle.f32_to_bf16(g.standard_normal(4096).astype(np.float32))
+    b = oracle.f32_to_bf16((g.standard_normal(4096) * 1e-2).astype(np.float32))
+    s = oracle.bf16_to_f32(a) + oracle.bf16_to_f32(b)  # numpy float32 add (one IEEE rounding)
+    assert np.array_equal(oracle.add_bf16(a, b), oracle.f32_to_bf16(s))
+
+
+def test_dsv2_join_rounds_twice_like_the_reference(oracle):
+    """bf16(f(bf16(routed)) + f(shared)) (nccl_backend.rs:544-545 then add_cuda): on these
+    inputs one rounding of routed + shared gives a different bf16, so a check against
+    the join can tell the two orders apart."""
+    routed = np.array([1.0 + 2 ** -8 + 2 ** -12, 1.0 + 2 ** -9], np.float32)
+    shared = oracle.f32_to_bf16(np.array([2 ** -8, 2 ** -9], np.float32))
+    two = oracle.dsv2_join(routed, shared)
+    one = oracle.add_f32_bf16(routed, shared)  # the single rounding kimi_add uses
+    # routed[0] -> bf16 1 + 2^-7 (above the tie), + 2^-8 = 1 + 3*2^-8 -> tie to even 1 + 2^-6
+    assert two[0] == 0x3F82
+    # one rounding: 1 + 2^-7 + 2^-12 -> 1 + 2^-7
+    assert one[0] == 0x3F81
+    # routed[1] -> 1.0 (tie to even), + 2^-9 -> 1.0; one rounding: 1 + 2^-8 -> tie to 1.0
+    assert two[1] == one[1] == 0x3F80
+    g = np.random.default_rng(22)
+    r = (g.standard_normal(100000) * 3).astype(np.float32)
+    sh = oracle.f32_to_bf16(g.standard_normal(100000).astype(np.float32))
+    j2 = oracle.dsv2_join(r, sh)
+    assert np.array_equal(j2, oracle.add_bf16(oracle.f32_to_bf16_n(r), sh))
+    assert (j2 != oracle.add_f32_bf16(r, sh)).mean() > 0.005  # the orders differ often
+
+
+# ---------------------------------------------------------------- CPU-baseline GEMM
+def test_fast_gemm_matches_checker_bit_for_bit_on_exact_sums(oracle):
+    """oracle_wna16_gemm_fast (the timed CPU baseline, 16 lane sums) gives the checker's
+    bits wherever every partial sum is exact, and stays within the fp32 bound elsewhere."""
+    g = np.random.default_rng(23)
+    E, N, K, T, topk = 4, 128, 1024, 12, 2
+    q = g.integers(-8, 8, size=(E, N, K))
+    s_bits = oracle.f32_to_bf16(np.ldexp(1.0, g.integers(-6, 2, (E, N, K // 32))).astype(np.float32))
+    a = oracle.f32_to_bf16(g.integers(-4, 5, (T, K)).astype(np.float32))
+    idx = g.integers(0, E, size=(T, topk)).astype(np.int32)
+    tw = g.random((T, topk)).astype(np.float32)
+    routing = oracle.align_block_size(idx.reshape(-1), 0, E, 16)
+    kw = dict(moe_block_size=16, top_k=topk, mul_topk_weights=True, size_m=T, size_n=N, size_k=K)
+    slow = oracle.wna16_gemm(a, _pack_ckpt(q), s_bits, routing, tw, **kw)
+    for threads in (1, 3):
+        fast = oracle.wna16_gemm(a, _pack_ckpt(q), s_bits, routing, tw, fast=True,
+                                 threads=threads, **kw)
+        assert np.array_equal(fast, slow)
+    # random scales and activations: within two bf16 roundings of each other
+    s_bits = oracle.f32_to_bf16((np.abs(g.standard_normal((E, N, K // 32))) * 0.003).astype(np.float32))
+    a = oracle.f32_to_bf16(g.standard_normal((T, K)).astype(np.float32))
+    slow = oracle.bf16_to_f32(oracle.wna16_gemm(a, _pack_ckpt(q), s_bits, routing, tw, **kw))
+    fast = oracle.bf16_to_f32(oracle.wna16_gemm(a, _pack_ckpt(q), s_bits, routing, tw, fast=True,
+                                                threads=2, **kw))
+    assert np.allclose(fast, slow, rtol=2 ** -6, atol=1e-5)
