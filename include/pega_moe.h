@@ -146,6 +146,23 @@ int pega_wna16_w13_swiglu(const uint16_t* input, uint16_t* act, float* partials,
                           int intermediate_dim, int size_k, int local_experts, int group_size,
                           int sm_count, hipStream_t stream);
 
+/* No reference counterpart; for callers that cannot allocate (code under HIP graph capture,
+ * serving loops and harnesses that forbid hipMalloc): pega_wna16_w13_swiglu without the
+ * partials workspace.  The K-split partials go to the library's static per-device scratch
+ * (2 MiB = 524,288 floats, held until the process ends; its device address is looked up once
+ * per device on the first call there).  Nothing in it needs clearing: every routed row of
+ * every K share is written before the SwiGLU kernel reads it.  Calls that overlap on one
+ * device race on the scratch.  A call whose wanted K split cannot hold two shares in the
+ * scratch (2 * size_m * top_k * 2 * intermediate_dim floats > 524,288) returns 801; every
+ * other call has the bits pega_wna16_w13_swiglu gives with a workspace of at least as many
+ * shares. */
+int pega_wna16_w13_swiglu_noalloc(const uint16_t* input, uint16_t* act, const uint8_t* b_qweight,
+                                  const uint16_t* b_scales, const int32_t* sorted_token_ids,
+                                  const int32_t* expert_ids, const int32_t* num_tokens_post_padded,
+                                  int sorted_token_ids_len, int moe_block_size, int top_k,
+                                  int size_m, int intermediate_dim, int size_k, int local_experts,
+                                  int group_size, int sm_count, hipStream_t stream);
+
 /* One problem of pega_wna16_prefill_pair: a grouped INT4 GEMM at a prefill block size (the
  * 128-row tile kernel), as pega_wna16_gemm (act NULL) or pega_wna16_w13_swiglu (act set)
  * would run it.  Plain pointers and sizes; 112 bytes on LP64. */

@@ -51,6 +51,7 @@ SIGNATURES = {
     "pega_weighted_topk_sum_f32": [_P, _P, _P, _I, _I, _I, _P],
     "pega_moe_combine_local_f32": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
     "pega_wna16_w13_swiglu": [_P, _P, _P, _LL, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P],
+    "pega_wna16_w13_swiglu_noalloc": [_P] * 7 + [_I] * 9 + [_P],
     "kimi_residual_add_scaled_f32_cuda": [_P, _P, _P, _F, _P, _I, _P],
     "kimi_residual_add_scaled_bf16_cuda": [_P, _P, _P, _F, _P, _I, _P],
     "kimi_add_f32_bf16_to_bf16_cuda": [_P, _P, _P, _I, _P],

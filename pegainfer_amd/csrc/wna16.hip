@@ -27,6 +27,7 @@
 // one 32-byte read.  Scales of n0 and n1 are adjacent in the permuted scale
 // row: index 8*(c%8) + 2*(c/8) (+1).
 #include <algorithm>
+#include <atomic>
 
 #include "common.h"
 #include "pega_moe.h"
@@ -968,12 +969,16 @@ int wna16_gemm(const uint16_t* input, uint16_t* output, float* c_tmp, long long 
 // K across workgroups; their fp32 partials go to `partials` and the SwiGLU
 // kernel sums them, so the split costs no extra launch and no cross-workgroup
 // synchronisation.
+// strict_scratch: `partials` is the library's fixed-size static scratch, so a call
+// whose wanted split does not fit two shares in it is rejected (kNotSupported)
+// instead of running unsplit.
 int wna16_w13_swiglu(const uint16_t* input, uint16_t* act, float* partials, long long partials_len,
                      const uint8_t* b_qweight, const uint16_t* b_scales,
                      const int32_t* sorted_token_ids, const int32_t* expert_ids,
                      const int32_t* num_tokens_post_padded, int sorted_token_ids_len,
                      int moe_block_size, int top_k, int size_m, int inter, int size_k,
-                     int local_experts, int group_size, int cu_count, hipStream_t stream) {
+                     int local_experts, int group_size, int cu_count, hipStream_t stream,
+                     bool strict_scratch = false) {
   if (!input || !act || !b_qweight || !b_scales || !sorted_token_ids || !expert_ids ||
       !num_tokens_post_padded)
     return fail(kInvalidValue, "w13_swiglu: null pointer");
@@ -1022,6 +1027,10 @@ int wna16_w13_swiglu(const uint16_t* input, uint16_t* act, float* partials, long
   if (sp > 16) sp = 16;
   if (sp > groups / 8) sp = groups / 8;
   const long long cap = partials ? partials_len / (routes * size_n) : 0;
+  if (strict_scratch && sp > 1 && cap < 2)
+    return fail(kNotSupported, "w13_swiglu (no-alloc): a %lld-share K split needs %lld bytes of "
+                "scratch for two shares; the static scratch holds %lld bytes", sp,
+                2LL * routes * size_n * 4, partials_len * 4);
   if (sp > cap) sp = cap;
   if (sp <= 1) {
     // No K split: a gate tile and its up tile in one workgroup of 2 WK waves,
@@ -1217,6 +1226,66 @@ PEGA_API int pega_wna16_w13_swiglu(const uint16_t* input, uint16_t* act, float* 
                                 sorted_token_ids_len, moe_block_size, top_k, size_m,
                                 intermediate_dim, size_k, local_experts, group_size, sm_count,
                                 stream);
+}
+
+// ---------------------------------------------------------------- no-allocation variant
+// The K-split partials of pega_wna16_w13_swiglu live in this fixed device array
+// instead of a caller workspace: 2 MiB (524,288 floats) per device, held until the
+// process ends.  Host code never passes `scratch` itself to a kernel (in host code the
+// name is only a stand-in for the device symbol): its device address is looked up once
+// per device, with that device current, and kept in g_scratch_addr.
+namespace {
+constexpr long long kScratchFloats = 1LL << 19;
+std::atomic<float*> g_scratch_addr[64];
+}  // namespace
+static __device__ __align__(256) float scratch[kScratchFloats];
+
+namespace {
+// This device's address of `scratch` (looked up on the first call on the device).
+float* scratch_address(int* status) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    *status = pega::fail(pega::kInvalidValue, "w13_swiglu (no-alloc): no current device");
+    return nullptr;
+  }
+  float* ptr = g_scratch_addr[dev].load(std::memory_order_acquire);
+  if (ptr != nullptr) return ptr;
+  void* addr = nullptr;
+  const hipError_t err = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+  if (err != hipSuccess || addr == nullptr) {
+    *status = pega::fail(pega::kLaunchFailed, "w13_swiglu (no-alloc): hipGetSymbolAddress: %s",
+                         hipGetErrorString(err));
+    return nullptr;
+  }
+  ptr = static_cast<float*>(addr);
+  g_scratch_addr[dev].store(ptr, std::memory_order_release);
+  return ptr;
+}
+}  // namespace
+
+// pega_wna16_w13_swiglu without the partials workspace (no reference counterpart; for
+// callers that cannot allocate, e.g. code under HIP graph capture): the K-split partials
+// go to the library's static per-device scratch.  Nothing in it needs clearing: every
+// routed row of every share is written before the SwiGLU kernel reads it.  Calls that
+// overlap on one device race on the scratch.  A call whose wanted split cannot hold two
+// shares in the scratch (routes * 2 * inter * 2 floats > 524,288) is rejected with 801.
+PEGA_API int pega_wna16_w13_swiglu_noalloc(const uint16_t* input, uint16_t* act,
+                                           const uint8_t* b_qweight, const uint16_t* b_scales,
+                                           const int32_t* sorted_token_ids,
+                                           const int32_t* expert_ids,
+                                           const int32_t* num_tokens_post_padded,
+                                           int sorted_token_ids_len, int moe_block_size,
+                                           int top_k, int size_m, int intermediate_dim,
+                                           int size_k, int local_experts, int group_size,
+                                           int sm_count, hipStream_t stream) {
+  int status = pega::kSuccess;
+  float* partials = scratch_address(&status);
+  if (partials == nullptr) return status;
+  return pega::wna16_w13_swiglu(input, act, partials, kScratchFloats, b_qweight, b_scales,
+                                sorted_token_ids, expert_ids, num_tokens_post_padded,
+                                sorted_token_ids_len, moe_block_size, top_k, size_m,
+                                intermediate_dim, size_k, local_experts, group_size, sm_count,
+                                stream, /*strict_scratch=*/true);
 }
 
 // Two prefill-size GEMMs in one launch (no reference symbol: the reference
