@@ -313,8 +313,13 @@ PEGA_API int gemm_graphsafe_cuda(const uint16_t* W, const uint16_t* X, uint16_t*
 }
 
 // No reference counterpart as one symbol: the shared expert's gate/up GEMM
-// followed by the SwiGLU of its bf16 output (moe_nccl.rs:107-123 runs
-// gemm_graphsafe_cuda then kimi_marlin_w13_swiglu_cuda), with the same bits.
+// followed by the SwiGLU of its bf16 output.  The reference runs
+// gemm_graphsafe_cuda, then silu_mul_fused_cuda (moe_nccl.rs:113-117 via
+// silu_mul_hs_fused_into; csrc/shared/fused_proj.cu:11-31): per element
+// bf16(f(bf16(g / (1 + e^-g))) * u) over the [N][2I] gate-then-up rows.  That
+// is the same arithmetic as kimi_marlin_w13_swiglu_cuda
+// (kimi_marlin_wna16.cu:345-361), which is what the epilogue here computes, so
+// the result has the same bits as that pair.
 PEGA_API int pega_dense_w13_swiglu(const uint16_t* W13, const uint16_t* X, uint16_t* act,
                                    int inter, int N, int K, hipStream_t stream) {
   if (inter > (1 << 29)) return fail(kInvalidValue, "pega_dense_w13_swiglu: bad inter=%d", inter);

@@ -171,7 +171,8 @@ class DenseW4A16:
 
 class KimiSharedExpert:
     """The Kimi-K2 shared expert, a bf16 dense MLP (moe_nccl.rs:107-123): gate/up
-    GEMM [2I, H] -> SwiGLU (gate first) -> down GEMM [H, I], bf16 `projected` out.
+    GEMM [2I, H] -> SwiGLU (gate first; silu_mul_fused_cuda,
+    csrc/shared/fused_proj.cu:11-31) -> down GEMM [H, I], bf16 `projected` out.
     The gate/up GEMM and the SwiGLU run as one launch (dense_w13_swiglu, the same
     bits as the reference's two calls)."""
 

@@ -637,7 +637,9 @@ def gemm_graphsafe(w: torch.Tensor, x: torch.Tensor, y: torch.Tensor) -> None:
 def dense_w13_swiglu(w13: torch.Tensor, x: torch.Tensor, act: torch.Tensor) -> None:
     """act = SwiGLU(bf16(X * W13^T)) in one launch: W13 [2I, K] bf16 (gate rows
     first), X [N, K], act [N, I].  The same bits as gemm_graphsafe followed by
-    kimi_marlin_w13_swiglu, the pair moe_nccl.rs:107-123 runs for the shared expert."""
+    silu_mul_fused_cuda, the pair the reference runs for the shared expert
+    (moe_nccl.rs:113-117; csrc/shared/fused_proj.cu:11-31), whose per-element
+    formula bf16(f(bf16(silu(g))) * u) is kimi_marlin_w13_swiglu's."""
     _ensure(_is_bf16(w13) and _is_bf16(x) and _is_bf16(act), "dense SwiGLU operands must be bf16")
     _ensure(w13.dim() == 2 and x.dim() == 2 and act.dim() == 2,
             "dense SwiGLU operands must be 2-D")
