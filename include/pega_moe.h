@@ -303,6 +303,21 @@ int pega_kimi_router_select(const float* logits, const float* e_score_correction
                             float* topk_weight, int32_t* topk_idx, int active_tokens,
                             int n_experts, int topk, float route_scale, hipStream_t stream);
 
+/* No reference symbol of its own: the router's select stage followed by the token -> expert
+ * permutation, in one launch of one workgroup (SURVEY's "router fused into the permutation":
+ * csrc/kimi_k2/kimi_router.cu:20-91 then csrc/kimi_k2/kimi_experts.cu:197-268, the pair
+ * experts.rs:508-848 issues).  Outputs equal pega_kimi_router_select followed by
+ * pega_moe_align_block_size (topk_idx / topk_weight over active_tokens rows, then the
+ * permutation of their active_tokens * topk routes), bit for bit, with the union of those two
+ * entry points' checks (status 1), and at most 4096 routes (801 above: a decode batch). */
+int pega_kimi_route_align(const float* logits, const float* e_score_correction_bias,
+                          float* topk_weight, int32_t* topk_idx, int32_t* sorted_token_ids,
+                          int32_t* expert_ids, int32_t* num_tokens_post_padded,
+                          uint32_t* expert_offsets, uint32_t* expert_cursor, int active_tokens,
+                          int n_experts, int topk, float route_scale, int global_start,
+                          int local_experts, int block_size, int max_padded_tokens,
+                          int max_m_blocks, hipStream_t stream);
+
 /* No reference C symbol: DeepSeek-V2-Lite softmax top-k sorted by expert id, restating
  * pegainfer-deepseek-v2-lite/src/host_ops.rs:388-412. */
 int pega_dsv2_router_select(const float* logits, float* topk_weight, int32_t* topk_idx,

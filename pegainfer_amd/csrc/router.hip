@@ -16,6 +16,7 @@
 //
 // Scores use e^x rounded from a double-precision exp, so that the CPU checker
 // reproduces them bit for bit and the selected indices agree exactly.
+#include "align_core.h"
 #include "common.h"
 #include "pega_moe.h"
 
@@ -23,6 +24,7 @@ namespace pega {
 namespace {
 
 constexpr int kMaxPerLane = 16;  // n_experts <= 64 * 16
+constexpr int kRouteAlignMaxRoutes = 4096;  // ids kept in LDS by the fused kernel
 
 // Order-preserving map of a float to u32 (for non-NaN values; -0 is folded
 // into +0 first, so equal floats give equal keys).  Key 0 lies below every
@@ -87,17 +89,16 @@ __device__ __forceinline__ float slot_value(const float (&v)[NS], int slot) {
   return r;
 }
 
-// One wave per token; lane l owns experts l, l+64, ... (NS slots per lane,
-// NS * 64 >= n_experts).
+// Token t's selection by one wave; lane l owns experts l, l+64, ... (NS slots
+// per lane, NS * 64 >= n_experts).  Writes the token's top-k ids and weights
+// and returns, on lane r < topk, the r-th selected id.
 template <int NS>
-__global__ void kimi_router_select_kernel(const float* __restrict__ logits,
-                                          const float* __restrict__ bias,
-                                          float* __restrict__ topk_weight,
-                                          int32_t* __restrict__ topk_idx, int tokens,
-                                          int n_experts, int topk, float route_scale) {
+__device__ __forceinline__ int kimi_select_token(const float* __restrict__ logits,
+                                                 const float* __restrict__ bias,
+                                                 float* __restrict__ topk_weight,
+                                                 int32_t* __restrict__ topk_idx, int t,
+                                                 int n_experts, int topk, float route_scale) {
   const int lane = threadIdx.x & 63;
-  const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  if (t >= tokens) return;  // whole waves leave
   float score[NS];
   uint32_t key[NS];
 #pragma unroll
@@ -132,6 +133,55 @@ __global__ void kimi_router_select_kernel(const float* __restrict__ logits,
     topk_idx[t * topk + lane] = my_i;
     topk_weight[t * topk + lane] = my_w * scale;
   }
+  return my_i;
+}
+
+// One wave per token.
+template <int NS>
+__global__ void kimi_router_select_kernel(const float* __restrict__ logits,
+                                          const float* __restrict__ bias,
+                                          float* __restrict__ topk_weight,
+                                          int32_t* __restrict__ topk_idx, int tokens,
+                                          int n_experts, int topk, float route_scale) {
+  const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (t >= tokens) return;  // whole waves leave
+  kimi_select_token<NS>(logits, bias, topk_weight, topk_idx, t, n_experts, topk, route_scale);
+}
+
+// The router's select stage and the token -> expert permutation in one
+// workgroup (decode batches): the 16 waves select tokens t, t + 16, ...,
+// keep the ids in LDS, and the workgroup then runs the permutation's counting
+// sort on them (align_core.h), so the ids make no round trip through memory
+// and the pair costs one launch.  Outputs are those of the select kernel
+// followed by the permutation kernel, bit for bit.
+template <int NS>
+__global__ __launch_bounds__(kAlignThreads) void kimi_route_align_kernel(
+    const float* __restrict__ logits, const float* __restrict__ bias,
+    float* __restrict__ topk_weight, int32_t* __restrict__ topk_idx,
+    int32_t* __restrict__ sorted_token_ids, int32_t* __restrict__ expert_ids,
+    int32_t* __restrict__ num_tokens_post_padded, uint32_t* __restrict__ expert_offsets,
+    uint32_t* __restrict__ expert_cursor, int tokens, int n_experts, int topk,
+    float route_scale, int global_start, int local_experts, int block_size,
+    int max_padded_tokens, int max_m_blocks) {
+  extern __shared__ __align__(16) unsigned char lds[];
+  const int route_elems = tokens * topk;
+  int32_t* s_idx = reinterpret_cast<int32_t*>(lds);  // [route_elems]
+  unsigned char* sort_lds = lds + ((route_elems * 4 + 15) & ~15);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int t = wave; t < tokens; t += kAlignWaves) {
+    const int sel = kimi_select_token<NS>(logits, bias, topk_weight, topk_idx, t, n_experts,
+                                          topk, route_scale);
+    if (lane < topk) s_idx[t * topk + lane] = sel;
+  }
+  __syncthreads();
+  auto expert_of = [&](int r) {
+    if (r >= route_elems) return -1;
+    const int e = s_idx[r] - global_start;
+    return (e >= 0 && e < local_experts) ? e : -1;
+  };
+  align_workgroup(expert_of, sort_lds, sorted_token_ids, expert_ids, num_tokens_post_padded,
+                  expert_offsets, expert_cursor, route_elems, local_experts, block_size,
+                  max_padded_tokens, max_m_blocks);
 }
 
 template <int NS>
@@ -215,6 +265,20 @@ struct KimiLaunch {
 };
 
 template <int NS>
+struct RouteAlignLaunch {
+  static void run(size_t lds, hipStream_t stream, const float* logits, const float* bias,
+                  float* w, int32_t* idx, int32_t* sorted_token_ids, int32_t* expert_ids,
+                  int32_t* ntp, uint32_t* expert_offsets, uint32_t* expert_cursor, int tokens,
+                  int n_experts, int topk, float scale, int global_start, int local_experts,
+                  int block_size, int max_padded_tokens, int max_m_blocks) {
+    hipLaunchKernelGGL(kimi_route_align_kernel<NS>, dim3(1), dim3(kAlignThreads), lds, stream,
+                       logits, bias, w, idx, sorted_token_ids, expert_ids, ntp, expert_offsets,
+                       expert_cursor, tokens, n_experts, topk, scale, global_start,
+                       local_experts, block_size, max_padded_tokens, max_m_blocks);
+  }
+};
+
+template <int NS>
 struct Dsv2Launch {
   static void run(dim3 grid, hipStream_t stream, const float* logits, float* w, int32_t* idx,
                   int tokens, int n_experts, int topk) {
@@ -246,6 +310,53 @@ PEGA_API int pega_kimi_router_select(const float* logits, const float* e_score_c
   launch_slots<KimiLaunch>(n_experts, dim3(grid), stream, logits, e_score_correction_bias,
                            topk_weight, topk_idx, active_tokens, n_experts, topk, route_scale);
   return launch_status("kimi_router_select");
+}
+
+// The select stage and the token -> expert permutation in one launch of one
+// workgroup (no reference counterpart as one symbol: kimi_router.cu:20-91
+// followed by kimi_experts.cu:197-268).  Same outputs, bit for bit, as
+// pega_kimi_router_select followed by pega_moe_align_block_size, with the
+// union of their argument checks; at most kRouteAlignMaxRoutes routes (decode
+// batches), kNotSupported above.
+PEGA_API int pega_kimi_route_align(const float* logits, const float* e_score_correction_bias,
+                                   float* topk_weight, int32_t* topk_idx,
+                                   int32_t* sorted_token_ids, int32_t* expert_ids,
+                                   int32_t* num_tokens_post_padded, uint32_t* expert_offsets,
+                                   uint32_t* expert_cursor, int active_tokens, int n_experts,
+                                   int topk, float route_scale, int global_start,
+                                   int local_experts, int block_size, int max_padded_tokens,
+                                   int max_m_blocks, hipStream_t stream) {
+  if (!logits || !e_score_correction_bias || !topk_weight || !topk_idx || !sorted_token_ids ||
+      !expert_ids || !num_tokens_post_padded || !expert_offsets || !expert_cursor)
+    return fail(kInvalidValue, "kimi_route_align: null pointer");
+  if (active_tokens <= 0 || n_experts <= 0 || n_experts > 64 * kMaxPerLane || topk <= 0 ||
+      topk > n_experts || topk > 64 || !(route_scale > 0.0f))
+    return fail(kInvalidValue, "kimi_route_align: bad shape tokens=%d experts=%d topk=%d",
+                active_tokens, n_experts, topk);
+  if (global_start < 0 || local_experts <= 0 || local_experts > kAlignMaxExperts)
+    return fail(kInvalidValue, "kimi_route_align: bad expert range start=%d E=%d", global_start,
+                local_experts);
+  if (!(block_size == 8 || (block_size >= 16 && block_size <= 64 && block_size % 16 == 0)))
+    return fail(kInvalidValue, "kimi_route_align: block_size %d not in {8,16,32,48,64}",
+                block_size);
+  const long long route_elems = static_cast<long long>(active_tokens) * topk;
+  if (route_elems > kRouteAlignMaxRoutes)
+    return fail(kNotSupported, "kimi_route_align: %lld routes (at most %d in one workgroup)",
+                route_elems, kRouteAlignMaxRoutes);
+  const long long req_padded = route_elems + static_cast<long long>(local_experts) * (block_size - 1);
+  const int required_blocks = ceil_div(static_cast<int>(req_padded), block_size);
+  if (max_padded_tokens < req_padded || max_m_blocks < required_blocks)
+    return fail(kInvalidValue,
+                "kimi_route_align: capacity too small (padded %d < %lld or blocks %d < %d)",
+                max_padded_tokens, req_padded, max_m_blocks, required_blocks);
+  const size_t lds = ((static_cast<size_t>(route_elems) * 4 + 15) & ~static_cast<size_t>(15)) +
+                     align_lds_bytes(local_experts);
+  launch_slots<RouteAlignLaunch>(n_experts, lds, stream, logits, e_score_correction_bias,
+                                 topk_weight, topk_idx, sorted_token_ids, expert_ids,
+                                 num_tokens_post_padded, expert_offsets, expert_cursor,
+                                 active_tokens, n_experts, topk, route_scale, global_start,
+                                 local_experts, block_size, max_padded_tokens, max_m_blocks);
+  return launch_status("kimi_route_align");
 }
 
 // DeepSeek-V2-Lite softmax top-k (no reference C symbol: the reference runs

@@ -655,6 +655,40 @@ def dense_w13_swiglu(w13: torch.Tensor, x: torch.Tensor, act: torch.Tensor) -> N
 # --------------------------------------------------------------------------
 # Routing select
 # --------------------------------------------------------------------------
+ROUTE_ALIGN_MAX_ROUTES = 4096  # routes the fused select + permutation keeps in one workgroup
+
+
+def kimi_route_align(workspace: KimiMarlinRouteWorkspace, logits: torch.Tensor, bias: torch.Tensor,
+                     topk_weight: torch.Tensor, topk_idx: torch.Tensor, active_tokens: int,
+                     global_expert_start: int, route_scale: float = 1.0) -> KimiMarlinRouting:
+    """The router's select stage and the token -> expert permutation in one launch
+    (pega_kimi_route_align): the outputs of kimi_router_select followed by
+    moe_align_block_size, bit for bit, for decode batches (at most 4096 routes)."""
+    ws = workspace
+    n_experts = logits.shape[-1]
+    _ensure(logits.dtype == torch.float32 and bias.dtype == torch.float32, "logits/bias f32")
+    _ensure(active_tokens > 0, "Kimi Marlin route active_tokens must be positive")
+    _ensure(active_tokens <= ws.max_active_tokens,
+            f"active_tokens {active_tokens} exceeds Kimi Marlin route workspace capacity "
+            f"{ws.max_active_tokens}")
+    route_elems = active_tokens * ws.topk
+    _ensure(route_elems <= ROUTE_ALIGN_MAX_ROUTES,
+            f"{route_elems} routes exceed the fused select + permutation's {ROUTE_ALIGN_MAX_ROUTES}")
+    _ensure(topk_idx.dtype == torch.int32 and topk_idx.numel() >= route_elems,
+            "topk_idx must be int32 covering active_tokens * topk")
+    _ensure(topk_weight.dtype == torch.float32 and topk_weight.numel() >= route_elems,
+            "topk_weight must be f32 covering active_tokens * topk")
+    _lib.call("pega_kimi_route_align", _ptr(logits), _ptr(bias), _ptr(topk_weight), _ptr(topk_idx),
+              _ptr(ws.sorted_token_ids), _ptr(ws.expert_ids), _ptr(ws.num_tokens_post_padded),
+              _ptr(ws.expert_offsets), _ptr(ws.expert_cursor), active_tokens, n_experts, ws.topk,
+              float(route_scale), global_expert_start, ws.local_experts, ws.block_size,
+              ws.max_padded_tokens, ws.max_m_blocks, _stream())
+    return KimiMarlinRouting(active_tokens, active_tokens, route_elems, global_expert_start,
+                             ws.block_size, ws.max_padded_tokens, ws.max_m_blocks, ws.topk,
+                             ws.local_experts, ws.sorted_token_ids, ws.expert_ids,
+                             ws.num_tokens_post_padded)
+
+
 def kimi_router_select(logits: torch.Tensor, bias: torch.Tensor, topk_weight: torch.Tensor,
                        topk_idx: torch.Tensor, active_tokens: int, topk: int = KIMI_K2_TOPK,
                        route_scale: float = 1.0) -> None:

@@ -73,12 +73,15 @@ def test_dense_gemm_entry_points_agree_and_reject(oracle):
     assert L.gemm_graphsafe_cuda(p(w), p(x), p(y2), M, 0, K, s) == 1
 
 
-def test_kimi_decode_layer_with_shared_expert(oracle):
+@pytest.mark.parametrize("T", [24, 3])
+def test_kimi_decode_layer_with_shared_expert(oracle, T):
     """Shared expert (bf16 gate/up and down), router select, routed experts and
-    the residual join, against the oracle's chain of the same stages."""
+    the residual join, against the oracle's chain of the same stages.  At 3 tokens
+    the layer routes through the fused select + permutation launch."""
     from pegainfer_amd import layer, ops, synth
-    E, H, I, T, SI = 48, 1024, 256, 24, 512
-    g = synth.rng(11, 1)
+    E, H, I, SI = 48, 1024, 256, 512
+    assert (T <= layer.FUSED_ROUTE_MAX_TOKENS) == (T == 3)
+    g = synth.rng(11, T)
     gate, up, down = (synth.int4_checkpoint(g, E, I, H), synth.int4_checkpoint(g, E, I, H),
                       synth.int4_checkpoint(g, E, H, I))
     gu = oracle.f32_to_bf16((g.standard_normal((2 * SI, H)) * 0.03).astype(np.float32))

@@ -1,6 +1,8 @@
 """GPU parity: token -> expert permutation (K1), DeepEP routing metadata (K9)
 and the router select stages, bit-exact against the oracle and the
 reference's known-answer vector."""
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -206,3 +208,65 @@ def test_kimi_router_noaux_tc_symbol(oracle, active, padded, seed):
     assert ok.mean() > 0.9
     ref_idx2, _ = oracle.kimi_router(ref_l[:active], bias, 8, 1.0)
     assert np.array_equal(ref_idx2[ok], ref_idx[ok])
+
+
+@pytest.mark.parametrize("tokens,bs,start,n_experts,E,seed", [
+    (1, 8, 0, 384, 48, 0), (3, 8, 48, 384, 48, 1), (16, 16, 0, 384, 48, 2),
+    (64, 16, 96, 384, 48, 3), (200, 32, 0, 384, 48, 4), (512, 64, 336, 384, 48, 5),
+    (64, 16, 0, 64, 64, 6), (37, 8, 10, 200, 17, 7)])
+def test_kimi_route_align_matches_two_launches(oracle, tokens, bs, start, n_experts, E, seed):
+    """The fused select + permutation (one workgroup) against the select kernel followed
+    by the permutation kernel: top-k ids and weights and every routing array bit for
+    bit, and the permutation against the oracle; outputs past the active rows and
+    the routing capacity are left as they were."""
+    from pegainfer_amd import ops
+    g = np.random.default_rng(70 + seed)
+    logits = dev(g.standard_normal((tokens, n_experts)).astype(np.float32))
+    bias = dev((g.standard_normal(n_experts) * 0.02).astype(np.float32))
+    ws_a = ops.KimiMarlinRouteWorkspace(tokens + 5, bs, topk=8, local_experts=E)
+    ws_b = ops.KimiMarlinRouteWorkspace(tokens + 5, bs, topk=8, local_experts=E)
+    for ws in (ws_a, ws_b):
+        for t in (ws.sorted_token_ids, ws.expert_ids, ws.expert_offsets, ws.expert_cursor):
+            t.fill_(-7)
+    w_a = torch.full(((tokens + 5) * 8,), -1.0, dtype=torch.float32, device="cuda")
+    w_b = w_a.clone()
+    i_a = torch.full(((tokens + 5) * 8,), -3, dtype=torch.int32, device="cuda")
+    i_b = i_a.clone()
+    ops.kimi_router_select(logits, bias, w_a, i_a, tokens)
+    ops.moe_align_block_size(ws_a, i_a, tokens, tokens, start)
+    ops.kimi_route_align(ws_b, logits, bias, w_b, i_b, tokens, start)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(i_a), host(i_b))
+    assert np.array_equal(host(w_a).view(np.uint32), host(w_b).view(np.uint32))
+    assert (host(i_b)[tokens * 8:] == -3).all() and (host(w_b)[tokens * 8:] == -1.0).all()
+    for name in ("sorted_token_ids", "expert_ids", "num_tokens_post_padded", "expert_offsets",
+                 "expert_cursor"):
+        assert np.array_equal(host(getattr(ws_a, name)), host(getattr(ws_b, name))), name
+    _check_against_oracle(oracle, ws_b, host(i_b)[:tokens * 8], start, E, bs)
+
+
+def test_kimi_route_align_rejections():
+    """Argument checks of the fused entry point: the select's and the permutation's
+    (status 1), and more than 4096 routes (801), all before any launch."""
+    from pegainfer_amd import _lib, ops
+    ws = ops.KimiMarlinRouteWorkspace(600, 64, topk=8, local_experts=48)
+    logits = torch.zeros(600, 384, dtype=torch.float32, device="cuda")
+    bias = torch.zeros(384, dtype=torch.float32, device="cuda")
+    w = torch.zeros(600 * 8, dtype=torch.float32, device="cuda")
+    i = torch.zeros(600 * 8, dtype=torch.int32, device="cuda")
+    L = _lib.lib()
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    base = [P(logits), P(bias), P(w), P(i), P(ws.sorted_token_ids), P(ws.expert_ids),
+            P(ws.num_tokens_post_padded), P(ws.expert_offsets), P(ws.expert_cursor)]
+
+    def call(tokens, n_experts=384, topk=8, scale=1.0, start=0, E=48, bs=64,
+             padded=ws.max_padded_tokens, blocks=ws.max_m_blocks):
+        return L.pega_kimi_route_align(*base, tokens, n_experts, topk, ctypes.c_float(scale),
+                                       start, E, bs, padded, blocks, None)
+    assert call(513) == 801                       # 4104 routes
+    assert call(0) == 1 and call(4, topk=0) == 1 and call(4, scale=0.0) == 1
+    assert call(4, n_experts=1025) == 1 and call(4, E=513) == 1 and call(4, bs=24) == 1
+    assert call(4, padded=10) == 1 and call(4, blocks=0) == 1
+    base[0] = ctypes.c_void_p(0)
+    assert call(4) == 1
+
