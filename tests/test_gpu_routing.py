@@ -213,7 +213,8 @@ def test_kimi_router_noaux_tc_symbol(oracle, active, padded, seed):
 @pytest.mark.parametrize("tokens,bs,start,n_experts,E,seed", [
     (1, 8, 0, 384, 48, 0), (3, 8, 48, 384, 48, 1), (16, 16, 0, 384, 48, 2),
     (64, 16, 96, 384, 48, 3), (200, 32, 0, 384, 48, 4), (512, 64, 336, 384, 48, 5),
-    (64, 16, 0, 64, 64, 6), (37, 8, 10, 200, 17, 7)])
+    (64, 16, 0, 64, 64, 6), (37, 8, 10, 200, 17, 7), (24, 16, 0, 384, 48, 8),
+    (40, 16, 0, 1000, 48, 9), (100, 32, 0, 1024, 64, 10)])
 def test_kimi_route_align_matches_two_launches(oracle, tokens, bs, start, n_experts, E, seed):
     """The fused select + permutation (one workgroup) against the select kernel followed
     by the permutation kernel: top-k ids and weights and every routing array bit for
