@@ -29,6 +29,28 @@ def test_swiglu_bit_exact(oracle, rows, inter):
     assert np.array_equal(got[fin], ref[fin])
 
 
+def test_swiglu_every_bf16_gate(oracle):
+    """Every bf16 gate value (all 65536 bit patterns), once with up = 1 (the result is
+    then bf16(silu) itself) and once with random up values, against the checker's
+    SwiGLU with the exact exponential: the kernels' fast exponential path, taken when
+    the fast silu is clear of a bf16 rounding midpoint, must give the same bits for
+    every gate they can be passed."""
+    from pegainfer_amd import ops
+    inter = 65536
+    gates = np.arange(inter, dtype=np.uint32).astype(np.uint16)
+    w13 = np.empty((2, 2 * inter), np.uint16)
+    w13[:, :inter] = gates
+    w13[0, inter:] = 0x3F80  # up = 1.0
+    w13[1, inter:] = _bf16_rand(np.random.default_rng(11), (inter,), 2.0)
+    out = torch.zeros(2, inter, dtype=torch.bfloat16, device="cuda")
+    ops.kimi_marlin_w13_swiglu(dev(w13), out, 2, inter)
+    got, ref = host(out), oracle.swiglu(w13, inter)
+    as_f32 = lambda b: (b.astype(np.uint32) << 16).view(np.float32)
+    nan_ref = np.isnan(as_f32(ref))
+    assert np.array_equal(np.isnan(as_f32(got)), nan_ref)
+    assert np.array_equal(got[~nan_ref], ref[~nan_ref])
+
+
 def test_swiglu_expanded_reads_rows_on_device(oracle):
     from pegainfer_amd import ops
     g = np.random.default_rng(9)
