@@ -88,15 +88,23 @@ __device__ __forceinline__ void align_workgroup(
 
   // 1. per-(wave, expert) route counts; the lowest lane of each peer set adds
   //    the set's size (peer sets have distinct experts, so no two lanes write
-  //    one counter)
+  //    one counter).  When the wave's steps fit one batch (up to 16 steps a
+  //    wave, 16384 routes) their experts and peer sets stay in registers for
+  //    the scatter, which then re-reads nothing.
+  const bool one_batch = s1 - s0 <= kAlignBatch;  // wave-uniform
+  int e_keep[kAlignBatch];
+  uint64_t peers_keep[kAlignBatch];
   for (int s = s0; s < s1; s += kAlignBatch) {
     int e[kAlignBatch];
 #pragma unroll
     for (int j = 0; j < kAlignBatch; ++j) e[j] = s + j < s1 ? expert_of((s + j) * 64 + lane) : -1;
 #pragma unroll
     for (int j = 0; j < kAlignBatch; ++j) {
+      e_keep[j] = e[j];
+      peers_keep[j] = 0;
       if (s + j < s1) {  // wave-uniform
         const uint64_t peers = same_expert_lanes(e[j], nbits);
+        peers_keep[j] = peers;
         if (e[j] >= 0 && (peers & below) == 0)
           my_cnt[e[j]] += static_cast<uint32_t>(__popcll(peers));
       }
@@ -149,11 +157,12 @@ __device__ __forceinline__ void align_workgroup(
   for (int s = s0; s < s1; s += kAlignBatch) {
     int e[kAlignBatch];
 #pragma unroll
-    for (int j = 0; j < kAlignBatch; ++j) e[j] = s + j < s1 ? expert_of((s + j) * 64 + lane) : -1;
+    for (int j = 0; j < kAlignBatch; ++j)
+      e[j] = one_batch ? e_keep[j] : (s + j < s1 ? expert_of((s + j) * 64 + lane) : -1);
 #pragma unroll
     for (int j = 0; j < kAlignBatch; ++j) {
       if (s + j >= s1) continue;  // wave-uniform
-      const uint64_t peers = same_expert_lanes(e[j], nbits);
+      const uint64_t peers = one_batch ? peers_keep[j] : same_expert_lanes(e[j], nbits);
       if (e[j] >= 0) {
         const uint32_t base = my_cnt[e[j]];
         const int pos = seg_start[e[j]] + static_cast<int>(base) + __popcll(peers & below);
