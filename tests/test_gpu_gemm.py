@@ -213,6 +213,52 @@ def test_w13_swiglu_fused_exact(oracle, E, T, topk, bs, inter, K, split_k):
     assert (got[~local] == 0x4040).all()  # bf16(3.0) untouched
 
 
+@pytest.mark.parametrize("seed", range(40))
+def test_gemm_and_w13_swiglu_shape_sweep_exact(oracle, seed):
+    """Seeded random shapes through both kernels: experts 1-20, tokens 1-400, top-k 1-8,
+    every block size, N and K from one to several tiles (odd chunk and gate-tile counts
+    included), with and without the top-k weight.  Inputs are exact (small-integer
+    activations, power-of-two scales), so every sum is exact and both the GEMM output
+    and W13 + SwiGLU must equal the oracle bit for bit; rows not routed here keep
+    their contents."""
+    from pegainfer_amd import ops
+    g = np.random.default_rng(900 + seed)
+    bs = int(g.choice([8, 16, 32, 48, 64]))
+    E = int(g.integers(1, 21))
+    T = int(g.integers(1, 401))
+    topk = int(min(g.choice([1, 2, 6, 8]), 2 * E))
+    K = 64 * int(g.integers(1, 11))
+    inter = 64 * int(g.integers(1, 6))
+    N = 2 * inter
+    mul = bool(g.integers(0, 2))
+    q = g.integers(-8, 8, size=(E, N, K))
+    scale_bits = oracle.f32_to_bf16(
+        (2.0 ** g.integers(-6, -2, size=(E, N, K // 32))).astype(np.float32))
+    a_bits = oracle.f32_to_bf16(g.integers(-2, 3, size=(T, K)).astype(np.float32))
+    idx = np.stack([g.permutation(2 * E)[:topk] for _ in range(T)]).astype(np.int32)
+    tw = oracle.bf16_to_f32(oracle.f32_to_bf16(g.random((T, topk)).astype(np.float32)))
+    what = f"seed={seed} bs={bs} E={E} T={T} topk={topk} N={N} K={K} mul={mul}"
+    got, ref = _run(oracle, E=E, N=N, K=K, T=T, topk=topk, bs=bs, mul=mul, a_bits=a_bits,
+                    q=q, scale_bits=scale_bits, idx=idx, tw=tw, extra_splits=4)
+    assert np.array_equal(got, ref), what
+    w, packed = _setup(E, N, K, q, scale_bits)
+    ws = ops.KimiMarlinRouteWorkspace(T, bs, topk=topk, local_experts=E)
+    routing = ops.moe_align_block_size(ws, dev(idx.reshape(-1)), T, T, 0)
+    gws = ops.KimiMarlinWna16Workspace(ws.max_m_blocks, N, bs, extra_splits=16)
+    act = torch.full((T * topk, inter), 3.0, dtype=torch.bfloat16, device="cuda")
+    ops.wna16_w13_swiglu(gws, routing, dev(a_bits), w, act, top_k=topk, size_m=T)
+    r = {k: host(v) for k, v in (("sorted_token_ids", routing.sorted_token_ids),
+                                 ("expert_ids", routing.expert_ids),
+                                 ("num_tokens_post_padded", routing.num_tokens_post_padded))}
+    ref13 = oracle.wna16_gemm(a_bits, packed, scale_bits, r, np.ones((T, topk), np.float32),
+                              moe_block_size=bs, top_k=topk, mul_topk_weights=False, size_m=T,
+                              size_n=N, size_k=K, threads=16)
+    local = idx.reshape(-1) < E
+    got_act = host(act)
+    assert np.array_equal(got_act[local], oracle.swiglu(ref13, inter)[local]), what
+    assert (got_act[~local] == 0x4040).all(), what
+
+
 def test_prefill_tile_scan_runs_and_gaps(oracle):
     """Prefill tiles found by the block-expert scan: an expert with two separate
     runs, runs shorter and longer than a tile, and blocks of expert -1 holding
