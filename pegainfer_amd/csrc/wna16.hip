@@ -210,6 +210,9 @@ __device__ __forceinline__ u32x4_t buf_load_b128(__amdgpu_buffer_rsrc_t r, uint3
 // words (th = 4*(c%8) + jj, w = c/8) as one 16-byte LDS read.  Slot layout:
 // word (th, w) of tile h at dword h*160 + w*32 + th (the 160 stride puts the
 // two tiles in opposite bank halves: writes and reads are conflict-free).
+// Each wave has two such slots, and a group's words are written one group
+// ahead of their use, so the write-to-read LDS round trip overlaps the
+// previous group's dequant instead of stalling its own.
 // Lanes whose activation row is not routed here read zeros through an
 // out-of-range buffer offset.  D groups per wave are in flight.
 // ---------------------------------------------------------------------------
@@ -230,7 +233,7 @@ __global__ __launch_bounds__(64 * WK * (kPair ? 2 : 1), 4) void wna16_decode_ker
   constexpr int kWaves = WK * (kPair ? 2 : 1);
   __shared__ int s_sid[32];
   __shared__ float s_red[kWaves][2 * NI][64];
-  __shared__ __align__(16) uint32_t s_w[kWaves][kSlotDwords];
+  __shared__ __align__(16) uint32_t s_w[kWaves][2][kSlotDwords];
 
   const int n_tiles = p.size_n >> 6;
   const int n_units = kPair ? (p.inter >> 6) : n_tiles;  // column units per K share
@@ -295,8 +298,10 @@ __global__ __launch_bounds__(64 * WK * (kPair ? 2 : 1), 4) void wna16_decode_ker
              8u * static_cast<uint32_t>(c >> 4)) * 2u
           : kOutOfRange;
 
-  uint32_t* slot_w = &s_w[wave][h * 160 + c];          // this lane's write column
-  const uint32_t* slot_r = &s_w[wave][h * 160 + 4 * c];  // this lane's 16-byte read
+  uint32_t* slot_w0 = &s_w[wave][0][h * 160 + c];          // this lane's write column
+  uint32_t* slot_w1 = &s_w[wave][1][h * 160 + c];
+  const uint32_t* slot_r0 = &s_w[wave][0][h * 160 + 4 * c];  // this lane's 16-byte read
+  const uint32_t* slot_r1 = &s_w[wave][1][h * 160 + 4 * c];
 
   auto load_group = [&](GroupRegs& r, int g) {
     g = min(max(g, 0), groups - 1);  // every scalar offset stays inside the expert
@@ -319,13 +324,16 @@ __global__ __launch_bounds__(64 * WK * (kPair ? 2 : 1), 4) void wna16_decode_ker
     __builtin_amdgcn_sched_barrier(0);
   }
 
-  auto compute_group = [&](const GroupRegs& r) {
-    // transpose the tile words into fragment order through this wave's slot
-    slot_w[0] = r.raw[0];
-    slot_w[32] = r.raw[1];
-    slot_w[64] = r.raw[2];
-    slot_w[96] = r.raw[3];
-    const u32x4_t fw = *reinterpret_cast<const u32x4_t*>(slot_r);
+  // transpose a group's tile words into fragment order through slot `par`
+  auto write_tr = [&](const GroupRegs& r, int par) {
+    uint32_t* sw = par ? slot_w1 : slot_w0;
+    sw[0] = r.raw[0];
+    sw[32] = r.raw[1];
+    sw[64] = r.raw[2];
+    sw[96] = r.raw[3];
+  };
+  auto compute_group = [&](const GroupRegs& r, int par) {
+    const u32x4_t fw = *reinterpret_cast<const u32x4_t*>(par ? slot_r1 : slot_r0);
     const uint32_t w4[4] = {fw[0], fw[1], fw[2], fw[3]};
     const BFrags b = make_b(w4, r.sp, dq);
     const bf16x8_t A = __builtin_bit_cast(bf16x8_t, r.a);
@@ -343,20 +351,30 @@ __global__ __launch_bounds__(64 * WK * (kPair ? 2 : 1), 4) void wna16_decode_ker
   // scheduler sinks all refills to the end of the unrolled round, and the
   // next round then opens with vmcnt(0), waiting out a full memory latency.
   // Pinned, group q waits only for its own loads while the D - 1 later
-  // groups' loads stay in flight (C3 W13 117.5 -> 113.3 us).
+  // groups' loads stay in flight (C3 W13 117.5 -> 113.3 us).  Step q first
+  // writes the transpose of the next group (ring slot q + 1, or slot 0, which
+  // step 0 refilled with the group D ahead), into the other LDS slot: a slot
+  // is rewritten only after the wave's read of it, and a wave's LDS
+  // operations complete in order.
   const int rounds = (g1 - g0) / D;
   int g = g0;
+  write_tr(slot[0], 0);
   for (int r = 0; r < rounds; ++r, g += D) {
 #pragma unroll
     for (int q = 0; q < D; ++q) {
-      compute_group(slot[q]);
+      write_tr(slot[(q + 1) % D], (q + 1) & 1);
+      compute_group(slot[q], q & 1);
       load_group(slot[q], min(g + q + D, g1 - 1));
       __builtin_amdgcn_sched_barrier(0);
     }
   }
 #pragma unroll
-  for (int q = 0; q < D - 1; ++q)
-    if (g + q < g1) compute_group(slot[q]);
+  for (int q = 0; q < D - 1; ++q) {
+    if (g + q < g1) {
+      if (q + 1 < D - 1 && g + q + 1 < g1) write_tr(slot[q + 1], (q + 1) & 1);
+      compute_group(slot[q], q & 1);
+    }
+  }
 
   // Deterministic reduction over the WK waves (fixed order 0..WK-1); only the
   // NI accumulator elements that hold rows < bs are exchanged, each the sum
