@@ -79,7 +79,11 @@ class RoutedExperts:
         reference_flow=True issues the reference's exact call sequence, zero-fills
         included; the default skips both zero-fills (rows of routes owned by other
         GPUs are never read: W2 reads only local rows, and the combine skips
-        non-local routes), which gives the same bits.
+        non-local routes) and fuses SwiGLU into W13.  The two give the same bits
+        whenever the fused and the plain W13 add over the same K shares (prefill
+        block sizes; decode grids of two or more W13 workgroups per CU with
+        K >= 4096); a small decode grid splits K differently, and a W13 sum may then
+        differ in the last fp32 bit.
         `w13_timer` (optional) exposes start()/stop(mark) and is called around the
         W13 GEMM launch so a caller can time that kernel with stream events.
         `companion` (optional, prefill block sizes only): a (W13, W2) pair of
@@ -106,7 +110,7 @@ class RoutedExperts:
                 w13_timer.stop(mark)
         elif not reference_flow:
             # SwiGLU in the W13 epilogue (gate and up tiles in one workgroup), routed rows
-            # only, same bits as W13 then SwiGLU
+            # only
             ops.wna16_w13_swiglu(self.gemm_ws, routing, hidden, self.w13, act, top_k=self.topk,
                                  size_m=T)
             if w13_timer is not None:

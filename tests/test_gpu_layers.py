@@ -343,3 +343,56 @@ def test_c5_every_block_exact_inputs(oracle):
         want = oracle.f32_to_bf16(oracle.bf16_to_f32(acc) * twb[rows][:, None])
         assert np.array_equal(ro[rows], want), f"W2 expert {e}"
     assert (ro[~local] == 0).all()
+
+
+@pytest.mark.parametrize("E", [48, 8])
+def test_routed_layer_edge_batches(oracle, E):
+    """The routed-expert layer at the batch edges, each against the oracle's composite and
+    against the reference's own call sequence (zero-fills, unfused SwiGLU, full combine), bit
+    for bit at the prefill block sizes: one token; a batch with no local route at all (the output must be zero); a
+    decode batch after a larger prefill-size one on the same buffers (stale rows of the
+    earlier call must not leak); the prefill block sizes at a few tokens.  E = 48 runs the
+    reference's kimi_* symbols, E = 8 the shape-general entries."""
+    from pegainfer_amd import ops, synth
+    H, I, topk = 512, 256, 8
+    gate, up, down = _kimi_weights(7, E, H, I)
+    w13p = np.concatenate([gate[0], up[0]], axis=1)
+    w13s = np.concatenate([gate[1], up[1]], axis=1)
+    g = np.random.default_rng(0xED6E)
+    # (tokens, block size, local routes?, what); each block size sees a larger batch
+    # before the smaller ones on the same layer buffers
+    cases = [(1, ops.kimi_marlin_block_size(1, topk, E), True, "one token, policy block size"),
+             (64, 16, True, "decode batch"), (1, 16, True, "one token after 64"),
+             (5, 16, False, "no local route"), (200, 64, True, "prefill size"),
+             (3, 64, True, "three tokens after 200, block 64"), (40, 32, True, "block 32"),
+             (7, 32, True, "seven tokens after 40, block 32"), (9, 8, True, "block 8")]
+    layers = {}
+    for T, bs, any_local, what in cases:
+        if bs not in layers:
+            layers[bs] = _routed_layer(gate, up, down, tokens=256, topk=topk, block_size=bs)
+        moe = layers[bs]
+        if not any_local:
+            idx = g.integers(E, 4 * E, size=(T, topk)).astype(np.int32)
+        else:
+            idx = np.stack([g.permutation(4 * E)[:topk] for _ in range(T)]).astype(np.int32)
+        w = g.random((T, topk), dtype=np.float32)
+        hidden = synth.normal_bf16(g, (T, H))
+        out = torch.full((T, H), np.nan, dtype=torch.float32, device="cuda")
+        moe.forward(dev(hidden), dev(idx), dev(w), out)
+        got = host(out)
+        ref_flow = torch.full((T, H), np.nan, dtype=torch.float32, device="cuda")
+        moe.forward(dev(hidden), dev(idx), dev(w), ref_flow, reference_flow=True)
+        if bs > 16:
+            # one wave covers all of K in both W13 forms: the same fp32 sums
+            assert np.array_equal(host(ref_flow).view(np.uint32), got.view(np.uint32)), what
+        else:
+            # these small decode grids split K one way in the fused W13 (across
+            # workgroups, or 8 waves) and another in the plain GEMM (16 waves, or 2)
+            assert_f32_close(got, host(ref_flow), rtol=2e-2, atol=2e-3, what=what)
+        if not any_local:
+            assert (got == 0).all(), what
+            continue
+        ref, _ = oracle.kimi_moe_layer(hidden, w13p, w13s, down[0], down[1], idx.reshape(-1), w,
+                                       global_start=0, local_experts=E, block_size=bs, hidden=H,
+                                       inter=I, topk=topk, threads=8)
+        assert_f32_close(got, ref, rtol=2e-2, atol=2e-3, what=f"{what} (T={T}, bs={bs})")
