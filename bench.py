@@ -125,6 +125,42 @@ def time_graph(torch, fn, steps, warmup, calls=GRAPH_CALLS):
     return e0.elapsed_time(e1) / (steps * calls)
 
 
+def attainable_read(torch, nbytes):
+    """The GPU's attainable HBM read rate, measured here: a plain streaming-read kernel
+    (pegainfer_amd/libpega_hbm_probe.so, measurement only) over `nbytes` per launch,
+    rotating through four buffers (more than the 256 MB MALL holds), 16 launches per
+    HIP graph; the best of three grid sizes.  Reported beside the roofline fraction as
+    what a kernel with no compute reaches on the same box."""
+    import ctypes
+    lib = ctypes.CDLL(os.path.join(ROOT, "pegainfer_amd", "libpega_hbm_probe.so"))
+    fn = lib.pega_hbm_read_probe
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_ulonglong, ctypes.c_void_p, ctypes.c_int,
+                   ctypes.c_void_p]
+    nbytes -= nbytes % 16
+    bufs = [torch.ones(nbytes // 4, dtype=torch.int32, device="cuda") for _ in range(4)]
+    best = None
+    for grid in (512, 1024, 2048):
+        out = torch.empty(grid * 256, dtype=torch.int32, device="cuda")
+        turn = [0]
+
+        def launch():
+            b = bufs[turn[0] % 4]
+            turn[0] += 1
+            rc = fn(b.data_ptr(), nbytes, out.data_ptr(), grid,
+                    torch.cuda.current_stream().cuda_stream)
+            if rc != 0:
+                raise RuntimeError("pega_hbm_read_probe failed")
+        ms = time_graph(torch, launch, 5, 2)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        if best is None or gbs > best["value"]:
+            best = dict(value=round(gbs, 1), unit="GB/s", grid=grid, launch_us=round(ms * 1e3, 2))
+    del bufs
+    torch.cuda.empty_cache()
+    best.update(kernel="hbm_read_kernel (contiguous chunk per workgroup, 16-byte "
+                       "non-temporal loads, 4 in flight per thread)", bytes_per_launch=nbytes)
+    return best
+
+
 def dev(torch, a, bf16=False):
     import numpy as np
     a = np.ascontiguousarray(a)
@@ -502,6 +538,9 @@ def main():
     want = lambda c: not only or c in only  # noqa: E731
     results = {}
     ctx = bench_c3(torch, args, results)
+    # right after C3, in the same clock and thermal state as its W13 timing
+    reach = attainable_read(torch, results["c3"]["w13_algorithmic_bytes"])
+    log(f"attainable HBM read (plain streaming kernel): {reach['value']:.0f} GB/s")
     for name, fn in (("c1", bench_c1), ("c2", bench_c2), ("c4", bench_c4), ("c5", bench_c5)):
         if want(name):
             fn(torch, args, results)
@@ -511,6 +550,9 @@ def main():
     roof = dict(bound="hbm", kernel="wna16_decode_kernel (W13 with SwiGLU epilogue, C3)",
                 achieved=round(c3["w13_gbs"], 1), peak=HBM_PEAK_GBS, unit="GB/s",
                 frac=round(c3["w13_gbs"] / HBM_PEAK_GBS, 4),
+                attainable_read=reach,
+                frac_of_attainable=round(c3["w13_gbs"] / reach["value"], 4),
+                layer_frac_of_attainable=round(c3["layer_gbs"] / reach["value"], 4),
                 traffic=load_traffic("wna16_w13_c3"),
                 algorithmic_bytes_per_launch=c3["w13_algorithmic_bytes"],
                 launch_us=round(c3["w13_us"], 2),
