@@ -44,6 +44,21 @@ def test_library_exports_every_declared_symbol():
         assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
 
 
+def test_hbm_probe_is_a_separate_library():
+    """bench.py's streaming-read probe (measurement only) lives in its own library and
+    rejects a misaligned or empty launch before touching the GPU; the expert-path
+    library does not carry it."""
+    from pegainfer_amd import _lib
+    probe = ctypes.CDLL(os.path.join(ROOT, "pegainfer_amd", "libpega_hbm_probe.so"))
+    fn = probe.pega_hbm_read_probe
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_ulonglong, ctypes.c_void_p, ctypes.c_int,
+                   ctypes.c_void_p]
+    assert fn(None, 1024, FAKE, 4, None) == 1
+    assert fn(FAKE, 1000, FAKE, 4, None) == 1  # not a multiple of 16 bytes
+    assert fn(FAKE, 1024, FAKE, 0, None) == 1
+    assert not hasattr(_lib.lib(), "pega_hbm_read_probe")
+
+
 def _call(name, *args):
     from pegainfer_amd import _lib
     return getattr(_lib.lib(), name)(*args), _lib.last_error()
