@@ -310,7 +310,7 @@ int pega_kimi_router_select(const float* logits, const float* e_score_correction
                             int n_experts, int topk, float route_scale, hipStream_t stream);
 
 /* No reference symbol of its own: the router's select stage followed by the token -> expert
- * permutation, in one launch of one workgroup (SURVEY's "router fused into the permutation":
+ * permutation, in one launch of one workgroup (the router fused into the permutation:
  * csrc/kimi_k2/kimi_router.cu:20-91 then csrc/kimi_k2/kimi_experts.cu:197-268, the pair
  * experts.rs:508-848 issues).  Outputs equal pega_kimi_router_select followed by
  * pega_moe_align_block_size (topk_idx / topk_weight over active_tokens rows, then the
