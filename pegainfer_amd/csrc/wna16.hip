@@ -426,28 +426,248 @@ __global__ __launch_bounds__(64 * WK * (kPair ? 2 : 1), 4) void wna16_decode_ker
   }
 }
 
+// ---------------------------------------------------------------------------
+// Decode kernel on v_mfma_f32_16x16x32_bf16, used at WK = 4 (C3's W13 pair,
+// the paired and plain W13 GEMMs alike, and its W2).  A block's 16 rows are the
+// MFMA's 16 rows, so the accumulators are 16 VGPRs per lane instead of the
+// 32-row form's 64 (whose rows 16..31 only fold k): 80 VGPRs, six waves per
+// SIMD instead of four, and three 8-wave W13 workgroups per CU instead of two.
+// A wave's 64 columns are four 16-column MFMA tiles.  Lane (n16 = cc + 8 a2,
+// kb = 2 kt + hf) takes the Marlin column pairs (w = 2 a2, cc) and
+// (w = 2 a2 + 1, cc) -- real columns 32 a2 + 8 j + cc for MFMA j -- and words
+// jj = 2 hf, 2 hf + 1 of k-tile kt, read from the same transpose slots as the
+// 32-row kernel with one 8-byte read per pair; its B fragments then hold
+// k 16 kt + 4 hf + {0..3, 8..11} (a word's nibbles are k 2jj + {0, 1, 8, 9}).
+// The activation fragment takes the same k set: each lane loads 16 bytes
+// (k 16 kt + 8 hf + 0..7) and a permlane16 swap exchanges the middle 8 bytes
+// with the lanes of the other k half.  The dequant is the 32-row kernel's; a
+// lane now scales four columns instead of two, and the two k halves' lanes
+// take one 8-byte scale load.  C3's W13 pair: 122.5 -> 119.2 us, W2 at WK = 4
+// instead of 2: 65.4 -> 64.0 us (three interleaved rounds, one box).
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float floatx4_t;
+
+__device__ __forceinline__ floatx4_t mfma16(bf16x8_t a, bf16x8_t b, floatx4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+struct GroupRegs16 {
+  u32x4_t raw;
+  uint32_t sp0, sp1;  // scales: pair A (n0, n1), pair B (n0, n1)
+  u32x4_t a;
+};
+
+template <int WK, int D, bool kPair = false>
+__global__ __launch_bounds__(64 * WK * (kPair ? 2 : 1), 6) void wna16_decode16_kernel(GemmArgs p) {
+  constexpr int kWaves = WK * (kPair ? 2 : 1);
+  __shared__ int s_sid[32];
+  __shared__ float s_red[kWaves][16][64];
+  __shared__ __align__(16) uint32_t s_w[kWaves][2][kSlotDwords];
+
+  const int n_tiles = p.size_n >> 6;
+  const int n_units = kPair ? (p.inter >> 6) : n_tiles;
+  const int split = blockIdx.x / n_units;
+  const int mb = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int valid_limit = p.size_m * p.top_k;
+  int sid = valid_limit;
+  if (tid < p.bs && mb * p.bs + tid < p.sorted_len) sid = p.sorted_ids[mb * p.bs + tid];
+  const int expert = __builtin_amdgcn_readfirstlane(p.expert_ids[mb]);
+  const int ntp = min(p.ntp[0], p.sorted_len);
+  if (ntp < (mb + 1) * p.bs || expert < 0 || expert >= p.num_experts) return;
+
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kw = wave % WK;
+  const int half = wave / WK;
+  const int nt = blockIdx.x % n_units + (kPair ? half * (p.inter >> 6) : 0);
+  if (tid < 32) s_sid[tid] = sid;
+  __syncthreads();
+
+  // loader view (as the 32x32 kernel): lane L holds word row th = L%32 of tile L/32
+  const int c = lane & 31, h = lane >> 5;
+  // MFMA view
+  const int n16 = lane & 15, kb = lane >> 4;
+  const int cc = n16 & 7, a2 = n16 >> 3;  // column pair index and pair-of-pairs
+  const int kt = kb >> 1, hf = kb & 1;    // k-tile within the group, k half
+  const int K = p.size_k, N = p.size_n;
+  const int groups = K >> 5;
+  const int gs0 = (groups * split) / p.splits, gs1 = (groups * (split + 1)) / p.splits;
+  const int g0 = gs0 + ((gs1 - gs0) * kw) / WK, g1 = gs0 + ((gs1 - gs0) * (kw + 1)) / WK;
+
+  const uint32_t expert_bytes = static_cast<uint32_t>(N) * static_cast<uint32_t>(K) / 2u;
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(
+      p.qweight + static_cast<long long>(expert) * (expert_bytes / 4u), expert_bytes);
+  const uint32_t tile_row_bytes = static_cast<uint32_t>(n_tiles) * 512u;
+  const uint32_t w_voff = static_cast<uint32_t>(h) * tile_row_bytes +
+                          static_cast<uint32_t>(nt) * 512u + static_cast<uint32_t>(c) * 16u;
+  const uint32_t w_step = 2u * tile_row_bytes;
+  const uint32_t scale_bytes = static_cast<uint32_t>(groups) * static_cast<uint32_t>(N) * 2u;
+  const __amdgpu_buffer_rsrc_t sr = make_rsrc(
+      p.scales + static_cast<long long>(expert) * groups * N, scale_bytes);
+  // pairs (2a2, cc) and (2a2 + 1, cc): bf16 scales 8cc + 4a2 + 0..3 of the tile
+  const uint32_t s_voff = (static_cast<uint32_t>(nt) * 64u + 8u * cc + 4u * a2) * 2u;
+  const uint32_t s_step = static_cast<uint32_t>(N) * 2u;
+  // activations: row n16, bytes 32 kt + 16 hf .. +15 of the group's 64
+  const int my_sid = s_sid[n16];
+  const __amdgpu_buffer_rsrc_t ar =
+      make_rsrc(p.input, static_cast<uint32_t>(p.size_m) * static_cast<uint32_t>(K) * 2u);
+  const uint32_t a_voff =
+      static_cast<unsigned>(my_sid) < static_cast<unsigned>(valid_limit)
+          ? (static_cast<uint32_t>(my_sid / p.top_k) * static_cast<uint32_t>(K)) * 2u +
+                32u * kt + 16u * hf
+          : kOutOfRange;
+
+  uint32_t* slot_w0 = &s_w[wave][0][h * 160 + c];
+  uint32_t* slot_w1 = &s_w[wave][1][h * 160 + c];
+  const int rd = kt * 160 + 64 * a2 + 4 * cc + 2 * hf;  // pair A's two words; pair B's +32
+  const uint32_t* slot_r0 = &s_w[wave][0][rd];
+  const uint32_t* slot_r1 = &s_w[wave][1][rd];
+
+  auto load_group = [&](GroupRegs16& r, int g) {
+    g = min(max(g, 0), groups - 1);
+    r.raw = buf_load_b128<kStream>(wr, w_voff, static_cast<uint32_t>(g) * w_step);
+    const auto sp = __builtin_amdgcn_raw_buffer_load_b64(sr, static_cast<int>(s_voff),
+                                                         static_cast<int>(g * s_step), kStream);
+    r.sp0 = sp[0];
+    r.sp1 = sp[1];
+    r.a = buf_load_b128(ar, a_voff, static_cast<uint32_t>(g) * 64u);
+  };
+
+  const DqConst dq = dq_consts();
+  floatx4_t acc[4] = {};
+  GroupRegs16 slot[D];
+#pragma unroll
+  for (int q = 0; q < D; ++q) {
+    load_group(slot[q], g0 + q < g1 ? g0 + q : g1 - 1);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  auto write_tr = [&](const GroupRegs16& r, int par) {
+    uint32_t* sw = par ? slot_w1 : slot_w0;
+    sw[0] = r.raw[0];
+    sw[32] = r.raw[1];
+    sw[64] = r.raw[2];
+    sw[96] = r.raw[3];
+  };
+  auto compute_group = [&](const GroupRegs16& r, int par) {
+    const uint32_t* sr_ = par ? slot_r1 : slot_r0;
+    const uint32_t wA0 = sr_[0], wA1 = sr_[1], wB0 = sr_[32], wB1 = sr_[33];
+    const ColScale sA0 = col_scale(bf_lo(r.sp0)), sA1 = col_scale(bf_hi(r.sp0));
+    const ColScale sB0 = col_scale(bf_lo(r.sp1)), sB1 = col_scale(bf_hi(r.sp1));
+    const WordPairs qa0 = dequant_word(wA0, sA0, sA1, dq);
+    const WordPairs qa1 = dequant_word(wA1, sA0, sA1, dq);
+    const WordPairs qb0 = dequant_word(wB0, sB0, sB1, dq);
+    const WordPairs qb1 = dequant_word(wB1, sB0, sB1, dq);
+    // activations: swap the middle 8 bytes with the other k half's lanes
+    const auto s0 = __builtin_amdgcn_permlane16_swap(r.a[0], r.a[2], false, false);
+    const auto s1 = __builtin_amdgcn_permlane16_swap(r.a[1], r.a[3], false, false);
+    const bf16x8_t A = hf ? as_bf16x8(s0[0], s1[0], r.a[2], r.a[3])
+                          : as_bf16x8(r.a[0], r.a[1], s0[1], s1[1]);
+    acc[0] = mfma16(A, as_bf16x8(qa0.n0_lo, qa1.n0_lo, qa0.n0_hi, qa1.n0_hi), acc[0]);
+    acc[1] = mfma16(A, as_bf16x8(qa0.n1_lo, qa1.n1_lo, qa0.n1_hi, qa1.n1_hi), acc[1]);
+    acc[2] = mfma16(A, as_bf16x8(qb0.n0_lo, qb1.n0_lo, qb0.n0_hi, qb1.n0_hi), acc[2]);
+    acc[3] = mfma16(A, as_bf16x8(qb0.n1_lo, qb1.n1_lo, qb0.n1_hi, qb1.n1_hi), acc[3]);
+  };
+
+  const int rounds = (g1 - g0) / D;
+  int g = g0;
+  write_tr(slot[0], 0);
+  for (int r = 0; r < rounds; ++r, g += D) {
+#pragma unroll
+    for (int q = 0; q < D; ++q) {
+      write_tr(slot[(q + 1) % D], (q + 1) & 1);
+      compute_group(slot[q], q & 1);
+      load_group(slot[q], min(g + q + D, g1 - 1));
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < D - 1; ++q) {
+    if (g + q < g1) {
+      if (q + 1 < D - 1 && g + q + 1 < g1) write_tr(slot[q + 1], (q + 1) & 1);
+      compute_group(slot[q], q & 1);
+    }
+  }
+
+  // element e = 4j + i of a lane: row 4 kb + i, column 32 a2 + 8 j + cc
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s_red[wave][4 * j + i][lane] = acc[j][i];
+  __syncthreads();
+
+  if constexpr (kPair) {
+    const int colb = (blockIdx.x % n_units) * 64 + 32 * a2 + cc;
+    for (int e = wave; e < 16; e += kWaves) {
+      float sg = 0.0f, su = 0.0f;
+#pragma unroll
+      for (int w = 0; w < WK; ++w) {
+        sg += s_red[w][e][lane];
+        su += s_red[WK + w][e][lane];
+      }
+      const int row = 4 * kb + (e & 3);
+      const int col = colb + 8 * (e >> 2);
+      if (row < p.bs) {
+        const int rsid = s_sid[row];
+        if (static_cast<unsigned>(rsid) < static_cast<unsigned>(valid_limit))
+          p.act[static_cast<long long>(rsid) * p.inter + col] =
+              swiglu_one(bf2f(f2bf(sg)), bf2f(f2bf(su)));
+      }
+    }
+    return;
+  }
+  const int colb = nt * 64 + 32 * a2 + cc;
+  for (int e = wave; e < 16; e += WK) {
+    float s = 0.0f;
+#pragma unroll
+    for (int w = 0; w < WK; ++w) s += s_red[w][e][lane];
+    const int row = 4 * kb + (e & 3);
+    const int n = colb + 8 * (e >> 2);
+    if (row < p.bs) {
+      const int rsid = s_sid[row];
+      if (static_cast<unsigned>(rsid) < static_cast<unsigned>(valid_limit)) {
+        if (p.partial)
+          p.partial[(static_cast<long long>(split) * valid_limit + rsid) * N + n] = s;
+        else
+          p.output[static_cast<long long>(rsid) * N + n] = epilogue_value(s, rsid, p);
+      }
+    }
+  }
+}
+
 constexpr int kDecodeDepth = 4;
 
+// WK = 4 runs the 16x16x32 kernel, the other share counts the 32-row one
+// (at 8 and 16 waves per workgroup the 16x16x32 form gains no occupancy and
+// its extra scale work cost C1/C2 2-4%).
 template <int WK>
 void launch_decode(const GemmArgs& args, int max_m_blocks, hipStream_t stream) {
   const dim3 grid(args.size_n / 64 * args.splits, max_m_blocks);
-  if (args.bs <= 8)
-    hipLaunchKernelGGL((wna16_decode_kernel<WK, 4, kDecodeDepth>), grid, dim3(64 * WK), 0, stream,
+  if constexpr (WK == 4) {
+    hipLaunchKernelGGL((wna16_decode16_kernel<WK, kDecodeDepth>), grid, dim3(64 * WK), 0, stream,
                        args);
-  else
-    hipLaunchKernelGGL((wna16_decode_kernel<WK, 8, kDecodeDepth>), grid, dim3(64 * WK), 0, stream,
-                       args);
+  } else {
+    if (args.bs <= 8)
+      hipLaunchKernelGGL((wna16_decode_kernel<WK, 4, kDecodeDepth>), grid, dim3(64 * WK), 0,
+                         stream, args);
+    else
+      hipLaunchKernelGGL((wna16_decode_kernel<WK, 8, kDecodeDepth>), grid, dim3(64 * WK), 0,
+                         stream, args);
+  }
 }
 
 template <int WK>
 void launch_decode_pair(const GemmArgs& args, int max_m_blocks, hipStream_t stream) {
   const dim3 grid(args.inter / 64, max_m_blocks);
-  if (args.bs <= 8)
-    hipLaunchKernelGGL((wna16_decode_kernel<WK, 4, kDecodeDepth, true>), grid, dim3(128 * WK), 0,
+  if constexpr (WK == 4) {
+    hipLaunchKernelGGL((wna16_decode16_kernel<WK, kDecodeDepth, true>), grid, dim3(128 * WK), 0,
                        stream, args);
-  else
-    hipLaunchKernelGGL((wna16_decode_kernel<WK, 8, kDecodeDepth, true>), grid, dim3(128 * WK), 0,
-                       stream, args);
+  } else {
+    if (args.bs <= 8)
+      hipLaunchKernelGGL((wna16_decode_kernel<WK, 4, kDecodeDepth, true>), grid, dim3(128 * WK),
+                         0, stream, args);
+    else
+      hipLaunchKernelGGL((wna16_decode_kernel<WK, 8, kDecodeDepth, true>), grid, dim3(128 * WK),
+                         0, stream, args);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -966,12 +1186,8 @@ int wna16_gemm(const uint16_t* input, uint16_t* output, float* c_tmp, long long 
     const long long wgs = est_blocks * n_tiles;
     int wk = wgs >= 4LL * cu_count ? 4 : (wgs >= 2LL * cu_count ? 8 : 16);
     while (wk > 4 && groups < wk) wk >>= 1;  // waves past the last group idle
-    // Short K with workgroups to spare (the decode W2): two waves of 32+
-    // groups each amortise the prologue and the reduction better than four
-    if (wk == 4 && groups < 4 * 32 && wgs >= 8LL * cu_count) wk = 2;
     if (max_m_blocks > 65535) return fail(kNotSupported, "wna16_gemm: too many m-blocks");
-    if (wk == 2) launch_decode<2>(args, max_m_blocks, stream);
-    else if (wk == 4) launch_decode<4>(args, max_m_blocks, stream);
+    if (wk == 4) launch_decode<4>(args, max_m_blocks, stream);
     else if (wk == 8) launch_decode<8>(args, max_m_blocks, stream);
     else launch_decode<16>(args, max_m_blocks, stream);
     return launch_status("wna16_gemm (decode)");
