@@ -131,9 +131,9 @@ int pega_wna16_gemm(const uint16_t* input, uint16_t* output, float* c_tmp, long 
  * are), and the W13 output never reaches HBM.  The bits are the pair's whenever both add the
  * fp32 products over the same K shares: always at block sizes 32-64 (one wave covers all of
  * K), and at block sizes 8/16 when the W13 GEMM has at least two workgroups per CU and K is at
- * least 4096 (C3's decode layer, for one).  Otherwise the shares differ (the K split below, or
- * 8 waves where the GEMM runs 16 or 4 where it runs 2), and the sums may differ from the
- * pair's in the last fp32 bit, within the same summation error bound.
+ * least 512 (C3's decode layer, for one).  Otherwise the shares differ (the K split below, or
+ * 8 waves where the GEMM runs 16), and the sums may differ from the pair's in the last fp32
+ * bit, within the same summation error bound.
  *  - Block size 8 or 16 (decode): when the (block, tile) units are too few to fill the GPU
  *    (one expert at batch 1-8), K is split across workgroups; the fp32 partials (partials:
  *    at least 2 * size_m * top_k * 2 * intermediate_dim floats for a split, more allows more

@@ -82,7 +82,7 @@ class RoutedExperts:
         non-local routes) and fuses SwiGLU into W13.  The two give the same bits
         whenever the fused and the plain W13 add over the same K shares (prefill
         block sizes; decode grids of two or more W13 workgroups per CU with
-        K >= 4096); a small decode grid splits K differently, and a W13 sum may then
+        K >= 512); a small decode grid splits K differently, and a W13 sum may then
         differ in the last fp32 bit.
         `w13_timer` (optional) exposes start()/stop(mark) and is called around the
         W13 GEMM launch so a caller can time that kernel with stream events.
