@@ -230,6 +230,7 @@ struct GroupRegs {
 // p.act (p.output and p.partial are not used).
 template <int WK, int NI, int D, bool kPair = false>
 __global__ __launch_bounds__(64 * WK * (kPair ? 2 : 1), 4) void wna16_decode_kernel(GemmArgs p) {
+  static_assert(D % 2 == 0, "the two transpose slots alternate with the ring position");
   constexpr int kWaves = WK * (kPair ? 2 : 1);
   __shared__ int s_sid[32];
   __shared__ float s_red[kWaves][2 * NI][64];
@@ -458,6 +459,7 @@ struct GroupRegs16 {
 
 template <int WK, int D, bool kPair = false>
 __global__ __launch_bounds__(64 * WK * (kPair ? 2 : 1), 6) void wna16_decode16_kernel(GemmArgs p) {
+  static_assert(D % 2 == 0, "the two transpose slots alternate with the ring position");
   constexpr int kWaves = WK * (kPair ? 2 : 1);
   __shared__ int s_sid[32];
   __shared__ float s_red[kWaves][16][64];
