@@ -547,7 +547,7 @@ def main():
     if not args.no_cpu:
         cpu_baseline_c3(ctx, results)
     c3 = results["c3"]
-    roof = dict(bound="hbm", kernel="wna16_decode_kernel (W13 with SwiGLU epilogue, C3)",
+    roof = dict(bound="hbm", kernel="wna16_decode16_kernel (W13 with SwiGLU epilogue, C3)",
                 achieved=round(c3["w13_gbs"], 1), peak=HBM_PEAK_GBS, unit="GB/s",
                 frac=round(c3["w13_gbs"] / HBM_PEAK_GBS, 4),
                 attainable_read=reach,
