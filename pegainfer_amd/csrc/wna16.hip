@@ -558,11 +558,12 @@ __global__ __launch_bounds__(64 * WK * (kPair ? 2 : 1), 6) void wna16_decode16_k
     const WordPairs qa1 = dequant_word(wA1, sA0, sA1, dq);
     const WordPairs qb0 = dequant_word(wB0, sB0, sB1, dq);
     const WordPairs qb1 = dequant_word(wB1, sB0, sB1, dq);
-    // activations: swap the middle 8 bytes with the other k half's lanes
+    // activations: swap the middle 8 bytes with the other k half's lanes (the odd
+    // 16-lane rows of the first operand with the even rows of the second), after
+    // which both halves find their fragment in the same registers
     const auto s0 = __builtin_amdgcn_permlane16_swap(r.a[0], r.a[2], false, false);
     const auto s1 = __builtin_amdgcn_permlane16_swap(r.a[1], r.a[3], false, false);
-    const bf16x8_t A = hf ? as_bf16x8(s0[0], s1[0], r.a[2], r.a[3])
-                          : as_bf16x8(r.a[0], r.a[1], s0[1], s1[1]);
+    const bf16x8_t A = as_bf16x8(s0[0], s1[0], s0[1], s1[1]);
     acc[0] = mfma16(A, as_bf16x8(qa0.n0_lo, qa1.n0_lo, qa0.n0_hi, qa1.n0_hi), acc[0]);
     acc[1] = mfma16(A, as_bf16x8(qa0.n1_lo, qa1.n1_lo, qa0.n1_hi, qa1.n1_hi), acc[1]);
     acc[2] = mfma16(A, as_bf16x8(qb0.n0_lo, qb1.n0_lo, qb0.n0_hi, qb1.n0_hi), acc[2]);
