@@ -444,7 +444,9 @@ __global__ __launch_bounds__(64 * WK * (kPair ? 2 : 1), 4) void wna16_decode_ker
 // with the lanes of the other k half.  The dequant is the 32-row kernel's; a
 // lane now scales four columns instead of two, and the two k halves' lanes
 // take one 8-byte scale load.  C3's W13 pair: 122.5 -> 119.2 us, W2 at WK = 4
-// instead of 2: 65.4 -> 64.0 us (three interleaved rounds, one box).
+// instead of 2: 65.4 -> 64.0 us (three interleaved rounds, one box).  The swap's
+// output goes into the fragment with no per-lane select (both k halves find the
+// swapped bytes in the same registers): 121.9 -> 117.0 us and 64.6 -> 62.9 us.
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float floatx4_t;
 
 __device__ __forceinline__ floatx4_t mfma16(bf16x8_t a, bf16x8_t b, floatx4_t c) {
