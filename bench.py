@@ -84,10 +84,29 @@ class EventTimer:
         return sum(s.elapsed_time(e) for s, e in self.pairs) / len(self.pairs)
 
 
-def time_steps(torch, fn, steps, warmup):
-    for _ in range(warmup):
+# An MI355X coming out of idle ramps its clocks over its first ~20 ms of load (the C3
+# graph: 204 us per layer over the first 20 replays after 5 warm-ups, 181 us from then
+# on, and 213 us again after 2 s idle), so every warm-up below also runs until the GPU
+# has been busy for WARM_MS: a short warm-up would leave part of the ramp in the timed
+# window.  The timed steps themselves are unchanged.
+WARM_MS = 50.0
+
+
+def warm(torch, fn, count):
+    """`count` untimed calls of `fn`, then more, one at a time, until WARM_MS of wall
+    time has passed since the first."""
+    t0 = time.perf_counter()
+    n = 0
+    while n < count or (time.perf_counter() - t0) * 1e3 < WARM_MS:
         fn()
+        n += 1
+        if n >= count:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
+
+
+def time_steps(torch, fn, steps, warmup):
+    warm(torch, fn, warmup)
     t0 = time.perf_counter()
     for _ in range(steps):
         fn()
@@ -113,9 +132,7 @@ def time_graph(torch, fn, steps, warmup, calls=GRAPH_CALLS):
     its full work."""
     from pegainfer_amd import layer
     graph = layer.capture_graph(lambda: [fn() for _ in range(calls)])
-    for _ in range(warmup):
-        graph.replay()
-    torch.cuda.synchronize()
+    warm(torch, graph.replay, warmup)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(torch.cuda.current_stream())
     for _ in range(steps):
@@ -207,9 +224,7 @@ def bench_c3(torch, args, results):
     log(f"C3: block size {bs}, {touched} experts touched, {local_routes} local routes, "
         f"{alg_bytes / 1e6:.1f} MB algorithmic")
     # Eager launches, W13 timed with events on its stream (the roofline kernel).
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
+    warm(torch, step, args.warmup)
     t0 = time.perf_counter()
     for _ in range(args.steps):
         step(record=True)
@@ -227,9 +242,7 @@ def bench_c3(torch, args, results):
         for _ in range(GRAPH_LAYERS - 1)]
 
     def replay_ms(graph, n):
-        for _ in range(args.warmup):
-            graph.replay()
-        torch.cuda.synchronize()
+        warm(torch, graph.replay, args.warmup)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(torch.cuda.current_stream())
         for _ in range(args.steps):
@@ -238,11 +251,26 @@ def bench_c3(torch, args, results):
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / (args.steps * n)
 
+    def replay_spread_us(graph, n, count=100):
+        """Median and p99 of the per-layer time over `count` replays, each between
+        its own pair of events (the mean above has no per-replay event in the way)."""
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(count + 1)]
+        ev[0].record(torch.cuda.current_stream())
+        for i in range(count):
+            graph.replay()
+            ev[i + 1].record(torch.cuda.current_stream())
+        torch.cuda.synchronize()
+        per = sorted(ev[i].elapsed_time(ev[i + 1]) * 1e3 / n for i in range(count))
+        return per[count // 2], per[min(count - 1, (99 * count + 99) // 100 - 1)]
+
     def step_layers():
         for m in layers:
             ops.kimi_router_select(logits, bias, tw, ti, T)
             m.forward(hidden, ti, tw, out)
-    ms = replay_ms(layer.capture_graph(step_layers), GRAPH_LAYERS)
+    layers_graph = layer.capture_graph(step_layers)
+    ms = replay_ms(layers_graph, GRAPH_LAYERS)
+    med_us, p99_us = replay_spread_us(layers_graph, GRAPH_LAYERS)
+    del layers_graph
     ms_one = replay_ms(layer.capture_graph(step), 1)
     del layers[1:]
     # The roofline kernel alone: the W13 + SwiGLU launch with the layer's routing,
@@ -262,7 +290,8 @@ def bench_c3(torch, args, results):
         workload="c3_kimi_moe_decode_t64", tokens=T, local_experts=E, hidden=H, inter=I, topk=8,
         block_size=bs, touched_experts=touched, local_routes=local_routes,
         algorithmic_bytes=alg_bytes, layer_us=ms * 1e3, layer_us_eager=eager_ms * 1e3,
-        graph_layers=GRAPH_LAYERS, layer_us_one_per_graph=ms_one * 1e3,
+        graph_layers=GRAPH_LAYERS, layer_us_median=med_us, layer_us_p99=p99_us,
+        layer_us_one_per_graph=ms_one * 1e3,
         layer_gbs=alg_bytes / (ms * 1e-3) / 1e9, w13_us=w13_graph_ms * 1e3,
         w13_us_in_eager_layer=w13_ms * 1e3,
         w13_algorithmic_bytes=w13_bytes, w13_gbs=w13_bytes / (w13_graph_ms * 1e-3) / 1e9,
@@ -350,9 +379,7 @@ def bench_c3_shared(torch, args, results, moe, normed, logits, bias):
                            args.warmup) / SHARED_COPIES
     del copies[1:]
     graph = layer.capture_graph(lambda: full.forward(hidden, normed, logits, bias, out))
-    for _ in range(args.warmup):
-        graph.replay()
-    torch.cuda.synchronize()
+    warm(torch, graph.replay, args.warmup)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(torch.cuda.current_stream())
     for _ in range(args.steps):
@@ -581,6 +608,8 @@ def main():
                            "copy of the weights)",
                     layer_us_eager=round(c3["layer_us_eager"], 2),
                     layer_us=round(c3["layer_us"], 2),
+                    layer_us_median=round(c3["layer_us_median"], 2),
+                    layer_us_p99=round(c3["layer_us_p99"], 2),
                     layer_us_one_per_graph=round(c3["layer_us_one_per_graph"], 2),
                     algorithmic_bytes=c3["algorithmic_bytes"]),
         roofline=roof,
