@@ -414,3 +414,43 @@ def test_gemm_decode_accepts_k_multiple_of_32(oracle, bs, K):
     got, ref = _run(oracle, E=E, N=N, K=K, T=T, topk=8, bs=bs, mul=False, a_bits=a_bits, q=q,
                     scale_bits=scale_bits, idx=idx, tw=np.ones((T, 8), np.float32))
     assert np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize("K", [64, 96, 1056, 2080])
+def test_decode16_uneven_and_empty_k_shares(oracle, K):
+    """The 16x16x32 decode kernel (4 K-share waves per tile, picked when the launch has at
+    least 4 workgroups per CU: here 77 m-blocks x 16 tiles = 1232 on 256 CUs) with group
+    counts that 4 does not divide (33, 65: shares of 8 and 9, 16 and 17 groups) and with
+    fewer groups than waves (2, 3: some waves add nothing), through the plain GEMM with the
+    top-k weight and through W13 + SwiGLU (616 gate/up pairs: the paired launch, 4 waves
+    per half).  Exact inputs, so both equal the oracle bit for bit."""
+    from pegainfer_amd import ops
+    E, T, topk, bs, inter = 48, 64, 8, 16, 512
+    N = 2 * inter
+    g = np.random.default_rng(4000 + K)
+    q = g.integers(-8, 8, size=(E, N, K))
+    scale_bits = oracle.f32_to_bf16(
+        (2.0 ** g.integers(-6, -2, size=(E, N, K // 32))).astype(np.float32))
+    a_bits = oracle.f32_to_bf16(g.integers(-2, 3, size=(T, K)).astype(np.float32))
+    idx = np.stack([g.permutation(2 * E)[:topk] for _ in range(T)]).astype(np.int32)
+    tw = oracle.bf16_to_f32(oracle.f32_to_bf16(g.random((T, topk)).astype(np.float32)))
+    got, ref = _run(oracle, E=E, N=N, K=K, T=T, topk=topk, bs=bs, mul=True, a_bits=a_bits,
+                    q=q, scale_bits=scale_bits, idx=idx, tw=tw, threads=16)
+    assert np.array_equal(got, ref), f"GEMM K={K}"
+    w, packed = _setup(E, N, K, q, scale_bits)
+    ws = ops.KimiMarlinRouteWorkspace(T, bs, topk=topk, local_experts=E)
+    routing = ops.moe_align_block_size(ws, dev(idx.reshape(-1)), T, T, 0)
+    assert ws.max_m_blocks * (N // 64) >= 4 * 256 and ws.max_m_blocks * (inter // 64) >= 2 * 256
+    gws = ops.KimiMarlinWna16Workspace(ws.max_m_blocks, N, bs)
+    act = torch.full((T * topk, inter), 3.0, dtype=torch.bfloat16, device="cuda")
+    ops.wna16_w13_swiglu(gws, routing, dev(a_bits), w, act, top_k=topk, size_m=T)
+    r = {k: host(v) for k, v in (("sorted_token_ids", routing.sorted_token_ids),
+                                 ("expert_ids", routing.expert_ids),
+                                 ("num_tokens_post_padded", routing.num_tokens_post_padded))}
+    ref13 = oracle.wna16_gemm(a_bits, packed, scale_bits, r, np.ones((T, topk), np.float32),
+                              moe_block_size=bs, top_k=topk, mul_topk_weights=False, size_m=T,
+                              size_n=N, size_k=K, threads=16)
+    local = idx.reshape(-1) < E
+    got_act = host(act)
+    assert np.array_equal(got_act[local], oracle.swiglu(ref13, inter)[local]), f"W13 K={K}"
+    assert (got_act[~local] == 0x4040).all()
