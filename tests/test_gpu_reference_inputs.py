@@ -16,6 +16,10 @@ is a multiple of 2^-11 and every partial sum stays below 2^13, so the W13 sums a
 fp32 in any order: W13, the fused SwiGLU and the top-k sum must match bit for bit.  W2 (whose
 inputs are the SwiGLU outputs) is held to the fp32 summation error bound before its top-k
 weight, and bit for bit after it given the unweighted bits.
+
+T = 4, 64, 160, 250, 400 and 4096 take block sizes 8, 16, 32, 48, 64 and 64 (the decode
+K-split path, the 16x16x32 decode kernel, and the prefill kernel at three block sizes up to
+the full C5 token count, where every one of the 32768 routes is local).
 """
 import numpy as np
 import pytest
@@ -69,7 +73,7 @@ def kimi_weights(oracle):
     return w13, w2
 
 
-@pytest.mark.parametrize("T", [4, 64, 160])
+@pytest.mark.parametrize("T", [4, 64, 160, 250, 400, 4096])
 def test_reference_tool_inputs(oracle, kimi_weights, T):
     from pegainfer_amd import layer, ops
     (w13, q13, s13), (w2, q2, s2) = kimi_weights
