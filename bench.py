@@ -46,6 +46,9 @@ def parse():
     p.add_argument("--calibrate-copy", action="store_true",
                    help="only run a plain 256 MiB device copy (reference kernel for the "
                         "FETCH_SIZE / WRITE_SIZE counter scale) and exit")
+    p.add_argument("--clock-ramp", action="store_true",
+                   help="only time the C3 graph in consecutive passes from a cold start "
+                        "(the evidence for WARM_MS) and exit")
     return p.parse_args()
 
 
@@ -58,6 +61,54 @@ def calibrate_copy(torch):
     torch.cuda.synchronize()
     print(json.dumps({"calibration": "copy", "bytes_read": n * 4, "bytes_written": n * 4,
                       "launches": 5}))
+
+
+def clock_ramp(torch):
+    """The C3 four-layer graph timed in consecutive passes of 20 replays: from 5 warm-up
+    replays, then again after 2 s idle.  The per-layer mean of each pass shows how long
+    the GPU takes to reach its steady clock (the reason for WARM_MS)."""
+    import numpy as np
+    from pegainfer_amd import layer, ops, synth
+    E, H, I, T = 48, 7168, 2048, 64
+    g = synth.rng(3, 1)
+    gate, up, down = (synth.int4_checkpoint(g, E, I, H), synth.int4_checkpoint(g, E, I, H),
+                      synth.int4_checkpoint(g, E, H, I))
+    hidden = dev(torch, synth.normal_bf16(synth.rng(3, 2), (T, H)), bf16=True)
+    logits = dev(torch, synth.rng(3, 3).standard_normal((T, 384), dtype=np.float32))
+    bias = torch.zeros(384, dtype=torch.float32, device="cuda")
+    tw = torch.zeros(T, 8, dtype=torch.float32, device="cuda")
+    ti = torch.zeros(T, 8, dtype=torch.int32, device="cuda")
+    out = torch.zeros(T, H, dtype=torch.float32, device="cuda")
+    layers = [layer.RoutedExperts(layer.package_w13(gate, up), layer.package_projection(*down),
+                                  max_tokens=T, topk=8, block_size=ops.kimi_marlin_block_size(T))
+              for _ in range(GRAPH_LAYERS)]
+
+    def step_layers():
+        for m in layers:
+            ops.kimi_router_select(logits, bias, tw, ti, T)
+            m.forward(hidden, ti, tw, out)
+    graph = layer.capture_graph(step_layers)
+
+    def passes(n, steps=20):
+        res = []
+        for _ in range(n):
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(torch.cuda.current_stream())
+            for _ in range(steps):
+                graph.replay()
+            e1.record(torch.cuda.current_stream())
+            torch.cuda.synchronize()
+            res.append(round(e0.elapsed_time(e1) * 1e3 / (steps * GRAPH_LAYERS), 1))
+        return res
+    for _ in range(5):
+        graph.replay()
+    cold = passes(12)
+    time.sleep(2.0)
+    idle = passes(6)
+    print(json.dumps({"clock_ramp": "c3 graph, per-layer us per pass of 20 replays "
+                                    "(4 layers each, about 15 ms)",
+                      "after_5_warmup_replays": cold, "after_2s_idle": idle}))
 
 
 class EventTimer:
@@ -561,6 +612,9 @@ def main():
         return
     import pegainfer_amd
     pegainfer_amd.load()
+    if args.clock_ramp:
+        clock_ramp(torch)
+        return
     only = set(x.strip() for x in args.only.split(",") if x.strip())
     want = lambda c: not only or c in only  # noqa: E731
     results = {}
