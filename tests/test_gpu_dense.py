@@ -191,3 +191,22 @@ def test_dense_w13_swiglu_three_and_four_token_blocks(oracle, I, N, K, rb):
     fused = torch.full((N, I), float("nan"), dtype=torch.bfloat16, device="cuda")
     ops.dense_w13_swiglu(w, x, fused)
     assert np.array_equal(host(fused), host(chain))
+
+
+@pytest.mark.parametrize("M,N,K", [(7168, 64, 2048), (4096, 57, 1024)])
+def test_dense_gemm_decode_sized_token_halves(oracle, M, N, K):
+    """Decode-sized token counts split into two 32-token workgroups with the short-K,
+    few-waves launch (dense.hip): the Kimi shared expert's down GEMM at 64 tokens, and
+    57 tokens (a partial last token block).  Random operands within the tolerance,
+    exact operands bit for bit."""
+    cu = torch.cuda.get_device_properties(0).multi_processor_count
+    assert _token_blocks(M, N, False, cu) == 2
+    g = np.random.default_rng(M + N + K)
+    w = oracle.f32_to_bf16((g.standard_normal((M, K)) * 0.02).astype(np.float32))
+    x = oracle.f32_to_bf16(g.standard_normal((N, K)).astype(np.float32))
+    assert_bf16_close(_gemm(w, x), oracle.dense_gemm(w, x), what=f"dense {M}x{N}x{K}")
+    we = oracle.f32_to_bf16(np.ldexp(g.integers(-8, 8, (M, K)), g.integers(-4, 0, (M, K)))
+                            .astype(np.float32))
+    xe = oracle.f32_to_bf16(g.integers(-3, 4, (N, K)).astype(np.float32))
+    ref = oracle.bf16_to_f32(xe).astype(np.float32) @ oracle.bf16_to_f32(we).astype(np.float32).T
+    assert np.array_equal(_gemm(we, xe), oracle.f32_to_bf16(ref))
