@@ -275,14 +275,14 @@ int dense_launch(const uint16_t* W, const uint16_t* X, void* Y, int rows, int M,
   const int stride = SWIGLU ? M : 16;
   // Few workgroups: more waves each, splitting K (at least one step a wave).
   // Once the grid has a workgroup per CU, fewer and longer K shares (at least
-  // 32 steps a wave) stream faster: Kimi's shared expert at 64 tokens, gate/up
-  // 7168 x 4096 with SwiGLU (256 workgroups) 20.4 -> 19.0 us at 4 waves instead
-  // of 16, down 2048 x 7168 (448 workgroups) 15.5 -> 11.8 us at 2 instead of 8
-  // (graph replays over 4 weight copies, one box).
+  // 64 steps a wave) stream faster: Kimi's shared expert at 64 tokens, gate/up
+  // 7168 x 4096 with SwiGLU (256 workgroups) 20.4 / 19.5 / 19.0 / 17.9 us at
+  // 16 / 8 / 4 / 2 waves, down 2048 x 7168 (448 workgroups) 15.5 / 12.5 / 11.8 /
+  // 11.5 us at 8 / 4 / 2 / 1 (graph replays over 4 weight copies, one box).
   const long long wgs = static_cast<long long>(grid.x) * grid.y;
   int wk = wgs <= cu ? 16 : (wgs <= 2LL * cu ? 8 : 4);
   if (wgs >= cu)
-    while (wk > 1 && K / 32 < 32 * wk) wk >>= 1;
+    while (wk > 1 && K / 32 < 64 * wk) wk >>= 1;
   while (wk > 1 && K / 32 < wk) wk >>= 1;
   switch (wk) {
     case 16: launch_dense<16, SWIGLU, F32>(mr, rb, grid, W, X, Y, M, N, K, stride, stream); break;
