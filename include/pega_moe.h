@@ -158,10 +158,11 @@ int pega_wna16_w13_swiglu(const uint16_t* input, uint16_t* act, float* partials,
  * (2 MiB = 524,288 floats, held until the process ends; its device address is looked up once
  * per device on the first call there).  Nothing in it needs clearing: every routed row of
  * every K share is written before the SwiGLU kernel reads it.  Calls that overlap on one
- * device race on the scratch.  A call whose wanted K split cannot hold two shares in the
- * scratch (2 * size_m * top_k * 2 * intermediate_dim floats > 524,288) returns 801; every
- * other call has the bits pega_wna16_w13_swiglu gives with a workspace of at least as many
- * shares. */
+ * device race on the scratch.  The output is pega_wna16_w13_swiglu's with a partials
+ * workspace of the scratch's size (partials_len = 524,288): the share count is capped by
+ * what the scratch holds, and a wanted K split it cannot hold two shares of runs unsplit, as
+ * the workspace entry does with a small workspace.  The current device must own `stream`
+ * (status 1 otherwise). */
 int pega_wna16_w13_swiglu_noalloc(const uint16_t* input, uint16_t* act, const uint8_t* b_qweight,
                                   const uint16_t* b_scales, const int32_t* sorted_token_ids,
                                   const int32_t* expert_ids, const int32_t* num_tokens_post_padded,

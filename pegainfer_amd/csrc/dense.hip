@@ -254,7 +254,7 @@ int dense_launch(const uint16_t* W, const uint16_t* X, void* Y, int rows, int M,
   if (M % 16 != 0 || K % 32 != 0)
     return fail(kNotSupported, "%s: M %% 16 and K %% 32 must be 0 (M=%d K=%d)", name, M, K);
   if ((reinterpret_cast<uintptr_t>(W) & 15u) != 0 || (reinterpret_cast<uintptr_t>(X) & 15u) != 0)
-    return fail(kInvalidValue, "%s: W and X must be 16-byte aligned", name);
+    return fail(kNotSupported, "%s: W and X must be 16-byte aligned", name);
   // X is addressed through one 32-bit buffer range that must stay below the
   // out-of-range offset, and so is a workgroup's W span: its 16 MR rows, or
   // with SwiGLU its gate rows through its up rows (I + 16 rows).  The size of

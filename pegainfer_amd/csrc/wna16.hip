@@ -1207,17 +1207,15 @@ int wna16_gemm(const uint16_t* input, uint16_t* output, float* c_tmp, long long 
 // few (m-block, tile) workgroups of a small batch are multiplied by splitting
 // K across workgroups; their fp32 partials go to `partials` and the SwiGLU
 // kernel sums them, so the split costs no extra launch and no cross-workgroup
-// synchronisation.
-// strict_scratch: `partials` is the library's fixed-size static scratch, so a call
-// whose wanted split does not fit two shares in it is rejected (kNotSupported)
-// instead of running unsplit.
+// synchronisation.  The share count is capped by what `partials` holds, and a
+// buffer that cannot hold two shares runs the launch unsplit; the bits then
+// depend only on `partials_len`, whichever entry point supplies the buffer.
 int wna16_w13_swiglu(const uint16_t* input, uint16_t* act, float* partials, long long partials_len,
                      const uint8_t* b_qweight, const uint16_t* b_scales,
                      const int32_t* sorted_token_ids, const int32_t* expert_ids,
                      const int32_t* num_tokens_post_padded, int sorted_token_ids_len,
                      int moe_block_size, int top_k, int size_m, int inter, int size_k,
-                     int local_experts, int group_size, int cu_count, hipStream_t stream,
-                     bool strict_scratch = false) {
+                     int local_experts, int group_size, int cu_count, hipStream_t stream) {
   if (!input || !act || !b_qweight || !b_scales || !sorted_token_ids || !expert_ids ||
       !num_tokens_post_padded)
     return fail(kInvalidValue, "w13_swiglu: null pointer");
@@ -1266,10 +1264,6 @@ int wna16_w13_swiglu(const uint16_t* input, uint16_t* act, float* partials, long
   if (sp > 16) sp = 16;
   if (sp > groups / 8) sp = groups / 8;
   const long long cap = partials ? partials_len / (routes * size_n) : 0;
-  if (strict_scratch && sp > 1 && cap < 2)
-    return fail(kNotSupported, "w13_swiglu (no-alloc): a %lld-share K split needs %lld bytes of "
-                "scratch for two shares; the static scratch holds %lld bytes", sp,
-                2LL * routes * size_n * 4, partials_len * 4);
   if (sp > cap) sp = cap;
   if (sp <= 1) {
     // No K split: a gate tile and its up tile in one workgroup of 2 WK waves,
@@ -1481,11 +1475,21 @@ static __device__ __align__(256) float scratch[kScratchFloats];
 
 namespace {
 // This device's address of `scratch` (looked up on the first call on the device).
-float* scratch_address(int* status) {
+// The kernels run on `stream`'s device, so that device must be the current one
+// (the lookup returns the current device's copy of the array).
+float* scratch_address(hipStream_t stream, int* status) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
     *status = pega::fail(pega::kInvalidValue, "w13_swiglu (no-alloc): no current device");
     return nullptr;
+  }
+  if (stream != nullptr) {
+    hipDevice_t sdev = -1;
+    if (hipStreamGetDevice(stream, &sdev) != hipSuccess || sdev != dev) {
+      *status = pega::fail(pega::kInvalidValue, "w13_swiglu (no-alloc): the stream belongs to "
+                           "device %d, not to the current device %d", sdev, dev);
+      return nullptr;
+    }
   }
   float* ptr = g_scratch_addr[dev].load(std::memory_order_acquire);
   if (ptr != nullptr) return ptr;
@@ -1506,8 +1510,9 @@ float* scratch_address(int* status) {
 // callers that cannot allocate, e.g. code under HIP graph capture): the K-split partials
 // go to the library's static per-device scratch.  Nothing in it needs clearing: every
 // routed row of every share is written before the SwiGLU kernel reads it.  Calls that
-// overlap on one device race on the scratch.  A call whose wanted split cannot hold two
-// shares in the scratch (routes * 2 * inter * 2 floats > 524,288) is rejected with 801.
+// overlap on one device race on the scratch.  The output equals pega_wna16_w13_swiglu's
+// with a partials workspace of the scratch's size (524,288 floats): as there, a split the
+// scratch cannot hold two shares of runs unsplit.  The current device must own `stream`.
 PEGA_API int pega_wna16_w13_swiglu_noalloc(const uint16_t* input, uint16_t* act,
                                            const uint8_t* b_qweight, const uint16_t* b_scales,
                                            const int32_t* sorted_token_ids,
@@ -1518,13 +1523,13 @@ PEGA_API int pega_wna16_w13_swiglu_noalloc(const uint16_t* input, uint16_t* act,
                                            int size_k, int local_experts, int group_size,
                                            int sm_count, hipStream_t stream) {
   int status = pega::kSuccess;
-  float* partials = scratch_address(&status);
+  float* partials = scratch_address(stream, &status);
   if (partials == nullptr) return status;
   return pega::wna16_w13_swiglu(input, act, partials, kScratchFloats, b_qweight, b_scales,
                                 sorted_token_ids, expert_ids, num_tokens_post_padded,
                                 sorted_token_ids_len, moe_block_size, top_k, size_m,
                                 intermediate_dim, size_k, local_experts, group_size, sm_count,
-                                stream, /*strict_scratch=*/true);
+                                stream);
 }
 
 // Two prefill-size GEMMs in one launch (no reference symbol: the reference

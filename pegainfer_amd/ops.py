@@ -658,6 +658,18 @@ def dense_w13_swiglu(w13: torch.Tensor, x: torch.Tensor, act: torch.Tensor) -> N
 ROUTE_ALIGN_MAX_ROUTES = 4096  # routes the fused select + permutation keeps in one workgroup
 
 
+def _ensure_router_inputs(logits: torch.Tensor, bias, active_tokens: int, n_experts: int) -> None:
+    """The select kernels read active_tokens rows of logits and n_experts biases on the
+    device: reject tensors that do not cover them."""
+    _ensure(logits.dtype == torch.float32, "logits must be f32")
+    _ensure(logits.is_contiguous(), "logits must be contiguous [tokens, n_experts]")
+    _ensure(logits.numel() >= active_tokens * n_experts,
+            f"logits must cover {active_tokens} rows of {n_experts} experts")
+    if bias is not None:
+        _ensure(bias.dtype == torch.float32, "bias must be f32")
+        _ensure(bias.numel() >= n_experts, f"bias must cover {n_experts} experts")
+
+
 def kimi_route_align(workspace: KimiMarlinRouteWorkspace, logits: torch.Tensor, bias: torch.Tensor,
                      topk_weight: torch.Tensor, topk_idx: torch.Tensor, active_tokens: int,
                      global_expert_start: int, route_scale: float = 1.0) -> KimiMarlinRouting:
@@ -666,8 +678,8 @@ def kimi_route_align(workspace: KimiMarlinRouteWorkspace, logits: torch.Tensor, 
     moe_align_block_size, bit for bit, for decode batches (at most 4096 routes)."""
     ws = workspace
     n_experts = logits.shape[-1]
-    _ensure(logits.dtype == torch.float32 and bias.dtype == torch.float32, "logits/bias f32")
     _ensure(active_tokens > 0, "Kimi Marlin route active_tokens must be positive")
+    _ensure_router_inputs(logits, bias, active_tokens, n_experts)
     _ensure(active_tokens <= ws.max_active_tokens,
             f"active_tokens {active_tokens} exceeds Kimi Marlin route workspace capacity "
             f"{ws.max_active_tokens}")
@@ -693,7 +705,11 @@ def kimi_router_select(logits: torch.Tensor, bias: torch.Tensor, topk_weight: to
                        topk_idx: torch.Tensor, active_tokens: int, topk: int = KIMI_K2_TOPK,
                        route_scale: float = 1.0) -> None:
     n_experts = logits.shape[-1]
-    _ensure(logits.dtype == torch.float32 and bias.dtype == torch.float32, "logits/bias f32")
+    _ensure_router_inputs(logits, bias, active_tokens, n_experts)
+    _ensure(topk_weight.dtype == torch.float32 and topk_weight.numel() >= active_tokens * topk,
+            "topk_weight must be f32 covering active_tokens * topk")
+    _ensure(topk_idx.dtype == torch.int32 and topk_idx.numel() >= active_tokens * topk,
+            "topk_idx must be int32 covering active_tokens * topk")
     _lib.call("pega_kimi_router_select", _ptr(logits), _ptr(bias), _ptr(topk_weight),
               _ptr(topk_idx), active_tokens, n_experts, topk, float(route_scale), _stream())
 
@@ -723,5 +739,10 @@ def kimi_k2_router_noaux_tc(hidden: torch.Tensor, gate_weight: torch.Tensor,
 def dsv2_router_select(logits: torch.Tensor, topk_weight: torch.Tensor, topk_idx: torch.Tensor,
                        tokens: int, topk: int = 6) -> None:
     n_experts = logits.shape[-1]
+    _ensure_router_inputs(logits, None, tokens, n_experts)
+    _ensure(topk_weight.dtype == torch.float32 and topk_weight.numel() >= tokens * topk,
+            "topk_weight must be f32 covering tokens * topk")
+    _ensure(topk_idx.dtype == torch.int32 and topk_idx.numel() >= tokens * topk,
+            "topk_idx must be int32 covering tokens * topk")
     _lib.call("pega_dsv2_router_select", _ptr(logits), _ptr(topk_weight), _ptr(topk_idx),
               tokens, n_experts, topk, _stream())

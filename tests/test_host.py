@@ -174,6 +174,18 @@ def test_router_noaux_tc_rejects_like_the_reference():
     assert call(ptrs=[FAKE] * 5 + [NULL])[0] == 1
     rc, msg = call(hidden=7168 + 16)
     assert rc == 801 and "K" in msg
+    # the MFMA logits GEMM reads hidden and gate_weight with 16-byte loads: a misaligned
+    # buffer is a layout this build does not support (801), as the header states
+    odd = ctypes.c_void_p(0x1008)
+    rc, msg = call(ptrs=[odd] + [FAKE] * 5)
+    assert rc == 801 and "aligned" in msg
+    rc, msg = call(ptrs=[FAKE, odd] + [FAKE] * 4)
+    assert rc == 801 and "aligned" in msg
+    for name in ("gemm_cuda", "gemm_graphsafe_cuda"):
+        rc, msg = _call(name, FAKE, odd, FAKE, 4096, 64, 7168, NULL)
+        assert rc == 801 and "aligned" in msg
+    rc, msg = _call("pega_dense_w13_swiglu", odd, FAKE, FAKE, 2048, 64, 7168, NULL)
+    assert rc == 801 and "aligned" in msg
 
 
 def test_dense_gemm_w_size_is_not_limited_only_its_workgroup_span():
@@ -374,3 +386,33 @@ def test_synth_routing_generators_are_seeded_and_shaped():
         assert 1 <= (row < 48).sum() <= 2
     counts = np.bincount(idx[idx < 48], minlength=48)
     assert counts.max() > 4 * max(1, np.median(counts))  # skewed
+
+
+def test_router_wrappers_reject_short_inputs_before_the_device():
+    """The select kernels read active_tokens rows of logits and n_experts biases on the
+    device: the host wrappers reject tensors that do not cover them (no launch)."""
+    import torch
+    from pegainfer_amd import ops
+    f32, i32 = torch.float32, torch.int32
+    ws = ops.KimiMarlinRouteWorkspace(4, 16, topk=8, local_experts=48, device="cpu")
+    ok = dict(logits=torch.zeros(4, 384, dtype=f32), bias=torch.zeros(384, dtype=f32),
+              topk_weight=torch.zeros(32, dtype=f32), topk_idx=torch.zeros(32, dtype=i32))
+
+    def route_align(**kw):
+        a = dict(ok, **kw)
+        ops.kimi_route_align(ws, a["logits"], a["bias"], a["topk_weight"], a["topk_idx"], 4, 0)
+
+    def select(**kw):
+        a = dict(ok, **kw)
+        ops.kimi_router_select(a["logits"], a["bias"], a["topk_weight"], a["topk_idx"], 4)
+
+    for fn in (route_align, select):
+        with pytest.raises(Exception, match="logits must cover"):
+            fn(logits=torch.zeros(3, 384, dtype=f32))
+        with pytest.raises(Exception, match="bias must cover"):
+            fn(bias=torch.zeros(383, dtype=f32))
+        with pytest.raises(Exception, match="topk_idx"):
+            fn(topk_idx=torch.zeros(31, dtype=i32))
+    with pytest.raises(Exception, match="logits must cover"):
+        ops.dsv2_router_select(torch.zeros(7, 64, dtype=f32), torch.zeros(48, dtype=f32),
+                               torch.zeros(48, dtype=i32), 8, 6)
