@@ -85,8 +85,7 @@ def clock_ramp(torch):
 
     def step_layers():
         for m in layers:
-            ops.kimi_router_select(logits, bias, tw, ti, T)
-            m.forward(hidden, ti, tw, out)
+            m.forward_from_logits(hidden, logits, bias, tw, ti, out)
     graph = layer.capture_graph(step_layers)
 
     def passes(n, steps=20):
@@ -260,8 +259,8 @@ def bench_c3(torch, args, results):
     timer = EventTimer(torch)
 
     def step(record=False):
-        ops.kimi_router_select(logits, bias, tw, ti, T)
-        moe.forward(hidden, ti, tw, out, w13_timer=timer if record else None)
+        moe.forward_from_logits(hidden, logits, bias, tw, ti, out,
+                                w13_timer=timer if record else None)
 
     step()
     torch.cuda.synchronize()
@@ -316,8 +315,7 @@ def bench_c3(torch, args, results):
 
     def step_layers():
         for m in layers:
-            ops.kimi_router_select(logits, bias, tw, ti, T)
-            m.forward(hidden, ti, tw, out)
+            m.forward_from_logits(hidden, logits, bias, tw, ti, out)
     layers_graph = layer.capture_graph(step_layers)
     ms = replay_ms(layers_graph, GRAPH_LAYERS)
     med_us, p99_us = replay_spread_us(layers_graph, GRAPH_LAYERS)
@@ -337,6 +335,16 @@ def bench_c3(torch, args, results):
                                       top_k=1, mul_topk_weights=True, size_m=T * 8),
         args.steps, args.warmup)
     w2_bytes = touched * W2_BYTES_PER_EXPERT + local_routes * I * 2 + local_routes * H * 2
+    # The layer's routing alone: the fused select + permutation launch it uses, and the
+    # select and permutation launches it replaces (same outputs, bit for bit).
+    route_fused_ms = time_graph(
+        torch, lambda: ops.kimi_route_align(moe.route_ws, logits, bias, tw, ti, T, 0),
+        args.steps, args.warmup)
+
+    def two_launches():
+        ops.kimi_router_select(logits, bias, tw, ti, T)
+        ops.moe_align_block_size(moe.route_ws, ti, T, T, 0)
+    route_two_ms = time_graph(torch, two_launches, args.steps, args.warmup)
     results["c3"] = dict(
         workload="c3_kimi_moe_decode_t64", tokens=T, local_experts=E, hidden=H, inter=I, topk=8,
         block_size=bs, touched_experts=touched, local_routes=local_routes,
@@ -347,12 +355,14 @@ def bench_c3(torch, args, results):
         w13_us_in_eager_layer=w13_ms * 1e3,
         w13_algorithmic_bytes=w13_bytes, w13_gbs=w13_bytes / (w13_graph_ms * 1e-3) / 1e9,
         w2_us=w2_graph_ms * 1e3, w2_algorithmic_bytes=w2_bytes,
-        w2_gbs=w2_bytes / (w2_graph_ms * 1e-3) / 1e9)
+        w2_gbs=w2_bytes / (w2_graph_ms * 1e-3) / 1e9,
+        route_fused_us=route_fused_ms * 1e3, route_two_launches_us=route_two_ms * 1e3)
     log(f"C3: layer {ms * 1e3:.1f} us graph-replayed ({GRAPH_LAYERS} layers per graph, "
         f"{results['c3']['layer_gbs']:.0f} GB/s), {ms_one * 1e3:.1f} us one layer per graph, "
         f"{eager_ms * 1e3:.1f} us eager; W13+SwiGLU {w13_graph_ms * 1e3:.1f} us alone "
         f"({results['c3']['w13_gbs']:.0f} GB/s; {w13_ms * 1e3:.1f} us in the eager layer), "
-        f"W2 {w2_graph_ms * 1e3:.1f} us alone ({results['c3']['w2_gbs']:.0f} GB/s)")
+        f"W2 {w2_graph_ms * 1e3:.1f} us alone ({results['c3']['w2_gbs']:.0f} GB/s); routing "
+        f"{route_fused_ms * 1e3:.1f} us fused, {route_two_ms * 1e3:.1f} us as two launches")
     bench_c3_shared(torch, args, results, moe, hidden, logits, bias)
     return dict(gate=gate, up=up, down=down, hidden=hidden_np, idx=idx,
                 w=tw.cpu().numpy(), bs=bs, alg_bytes=alg_bytes)

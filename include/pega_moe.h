@@ -311,12 +311,15 @@ int pega_kimi_router_select(const float* logits, const float* e_score_correction
                             int n_experts, int topk, float route_scale, hipStream_t stream);
 
 /* No reference symbol of its own: the router's select stage followed by the token -> expert
- * permutation, in one launch of one workgroup (the router fused into the permutation:
+ * permutation, in one launch (the router fused into the permutation:
  * csrc/kimi_k2/kimi_router.cu:20-91 then csrc/kimi_k2/kimi_experts.cu:197-268, the pair
  * experts.rs:508-848 issues).  Outputs equal pega_kimi_router_select followed by
  * pega_moe_align_block_size (topk_idx / topk_weight over active_tokens rows, then the
  * permutation of their active_tokens * topk routes), bit for bit, with the union of those two
- * entry points' checks (status 1), and at most 4096 routes (801 above: a decode batch). */
+ * entry points' checks (status 1), and at most 4096 routes (801 above: a decode batch).  Above
+ * four tokens the select runs in several workgroups and the last to finish sorts; they count
+ * themselves in on a library-wide per-device counter, so launches of this entry point or of
+ * pega_dsv2_route_align that overlap on one device race. */
 int pega_kimi_route_align(const float* logits, const float* e_score_correction_bias,
                           float* topk_weight, int32_t* topk_idx, int32_t* sorted_token_ids,
                           int32_t* expert_ids, int32_t* num_tokens_post_padded,
@@ -324,6 +327,19 @@ int pega_kimi_route_align(const float* logits, const float* e_score_correction_b
                           int n_experts, int topk, float route_scale, int global_start,
                           int local_experts, int block_size, int max_padded_tokens,
                           int max_m_blocks, hipStream_t stream);
+
+/* No reference symbol of its own: the DeepSeek-V2-Lite router (softmax top-k ordered by expert
+ * id: pegainfer-deepseek-v2-lite/src/host_ops.rs:388-412, csrc/dsv2_lite/dsv2_lite_moe.cu:41-129)
+ * followed by the token -> expert permutation, in one launch.  Outputs equal
+ * pega_dsv2_router_select followed by pega_moe_align_block_size, bit for bit; the checks and
+ * limits of pega_kimi_route_align (at most 4096 routes, 801 above), and the same race between
+ * overlapping launches on one device. */
+int pega_dsv2_route_align(const float* logits, float* topk_weight, int32_t* topk_idx,
+                          int32_t* sorted_token_ids, int32_t* expert_ids,
+                          int32_t* num_tokens_post_padded, uint32_t* expert_offsets,
+                          uint32_t* expert_cursor, int tokens, int n_experts, int topk,
+                          int global_start, int local_experts, int block_size,
+                          int max_padded_tokens, int max_m_blocks, hipStream_t stream);
 
 /* No reference C symbol: DeepSeek-V2-Lite softmax top-k sorted by expert id, restating
  * pegainfer-deepseek-v2-lite/src/host_ops.rs:388-412. */

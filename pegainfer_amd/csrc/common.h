@@ -70,6 +70,46 @@ __device__ __forceinline__ float exp_exact_f32(float x) {
   return static_cast<float>(::exp(static_cast<double>(x)));
 }
 
+// exp_exact_f32(x), bit for bit, at about half its cost.  For |x| <= 80 a
+// degree-11 Taylor polynomial on r = x - n ln2 (|r| <= 0.347, ln2 split so that
+// n * ln2_hi is exact) gives a = e^x within 2^-46.5 relative (truncation
+// 0.347^12 / 12! / e^-0.347 = 2^-46.7, plus the Horner roundings).  The
+// library's double exp is within one double ulp (2^-52) of e^x, so the two
+// doubles differ by less than g = 2^-45 a.
+// Both then round to the same float f = RN(a) unless a rounding midpoint of
+// f's neighbourhood lies within g of a: that is checked exactly (a - f is exact
+// in double), and only then, about once in 2^20 calls, does the double exp run.
+__device__ __forceinline__ float exp_exact_f32_fast(float x) {
+  if (!(__builtin_fabsf(x) <= 80.0f)) return exp_exact_f32(x);  // NaN too
+  const double xd = static_cast<double>(x);
+  const double n = __builtin_rint(xd * 1.4426950408889634);
+  double r = __builtin_fma(-n, 0x1.62e42fefa3800p-1, xd);  // ln2_hi: 43 bits, n * ln2_hi exact
+  r = __builtin_fma(-n, 0x1.ef35793c76730p-45, r);          // ln2_lo
+  double p = 1.0 / 39916800.0;                               // 1/11!
+  p = __builtin_fma(p, r, 1.0 / 3628800.0);
+  p = __builtin_fma(p, r, 1.0 / 362880.0);
+  p = __builtin_fma(p, r, 1.0 / 40320.0);
+  p = __builtin_fma(p, r, 1.0 / 5040.0);
+  p = __builtin_fma(p, r, 1.0 / 720.0);
+  p = __builtin_fma(p, r, 1.0 / 120.0);
+  p = __builtin_fma(p, r, 1.0 / 24.0);
+  p = __builtin_fma(p, r, 1.0 / 6.0);
+  p = __builtin_fma(p, r, 0.5);
+  p = __builtin_fma(p, r, 1.0);
+  p = __builtin_fma(p, r, 1.0);
+  const double a = __builtin_ldexp(p, static_cast<int>(n));
+  const float f = static_cast<float>(a);
+  const double d = a - static_cast<double>(f);  // exact: a and f within one float ulp
+  const uint32_t fb = __builtin_bit_cast(uint32_t, f);
+  // half the float ulp above f, and below it (a quarter when f is a power of two)
+  const double half_up = __builtin_bit_cast(
+      double, static_cast<uint64_t>(((fb >> 23) & 0xffu) + 1023u - 151u) << 52);
+  const double half_dn = (fb & 0x7fffffu) ? half_up : 0.5 * half_up;
+  const double g = a * 0x1p-45;
+  if (d + g < half_up && d - g > -half_dn) return f;
+  return exp_exact_f32(x);
+}
+
 // SwiGLU of one column pair: bf16( f(bf16(g / (1 + e^-g))) * u ), g = gate,
 // u = up (pegainfer-kernels/csrc/kimi_k2/kimi_marlin_wna16.cu:345-361), with
 // e^-g the exp_exact_f32 value (the CPU checker's definition).

@@ -66,73 +66,75 @@ __device__ __forceinline__ float lane_value(float v, int lane) {
                             __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
 }
 
-// Index of the largest key over the wave's NS x 64 slots, ties to the lower
-// index (expert id lane + 64 j); the result is wave-uniform.
+// Top-k of the wave's NS x 64 keys (expert id lane + 64 j), largest first,
+// equal keys to the lower id.  Returns, on lane r < topk, the r-th selected
+// id; the selected keys are cleared.  A round is one DPP max-reduction of the
+// lanes' best keys; the holders of the maximum are a ballot, and only when
+// several lanes hold it (equal keys) does a second reduction pick the lowest
+// id (a lane's own slots are scanned from j = 0, so its candidate is its
+// lowest id with that key).
 template <int NS>
-__device__ __forceinline__ int wave_argmax(const uint32_t (&key)[NS], int lane) {
-  uint32_t best = 0;
-  int bj = 0;
+__device__ __forceinline__ int wave_topk_ids(uint32_t (&key)[NS], int lane, int topk) {
+  int my_sel = 0;
+  for (int r = 0; r < topk; ++r) {
+    uint32_t best = key[0];
 #pragma unroll
-  for (int j = 0; j < NS; ++j)
-    if (key[j] > best) { best = key[j]; bj = j; }  // strict: the lower slot keeps a tie
-  const uint32_t top = wave_reduce_u32(best, MaxU32{});
-  const uint32_t cand = best == top ? static_cast<uint32_t>(lane + 64 * bj) : 0xffffffffu;
-  return static_cast<int>(wave_reduce_u32(cand, MinU32{}));
+    for (int j = 1; j < NS; ++j) best = best > key[j] ? best : key[j];
+    const uint32_t top = wave_reduce_u32(best, MaxU32{});
+    int jsel = NS;
+#pragma unroll
+    for (int j = NS - 1; j >= 0; --j)
+      if (key[j] == top) jsel = j;
+    const uint64_t holders = __ballot(jsel < NS);
+    int win;
+    if (__popcll(holders) == 1) {
+      const int wl = __builtin_ctzll(holders);
+      win = __builtin_amdgcn_readlane(jsel * 64 + lane, wl);
+    } else {
+      const uint32_t cand = jsel < NS ? static_cast<uint32_t>(jsel * 64 + lane) : 0xffffffffu;
+      win = static_cast<int>(wave_reduce_u32(cand, MinU32{}));
+    }
+    const int wj = win >> 6;
+    if (lane == (win & 63)) {
+#pragma unroll
+      for (int j = 0; j < NS; ++j)
+        if (j == wj) key[j] = 0;
+    }
+    if (lane == r) my_sel = win;
+  }
+  return my_sel;
 }
 
-template <int NS>
-__device__ __forceinline__ float slot_value(const float (&v)[NS], int slot) {
-  float r = 0.0f;
-#pragma unroll
-  for (int j = 0; j < NS; ++j)
-    if (j == slot) r = v[j];
-  return r;
+// Kimi router score of logit l: 1 / (1 + e^-l), e^-l rounded from a double exp.
+__device__ __forceinline__ float kimi_score(float l) {
+  return 1.0f / (1.0f + exp_exact_f32_fast(-l));
 }
 
 // Token t's selection by one wave; lane l owns experts l, l+64, ... (NS slots
-// per lane, NS * 64 >= n_experts).  Writes the token's top-k ids and weights
-// and returns, on lane r < topk, the r-th selected id.
+// per lane, NS * 64 >= n_experts).  Writes the token's top-k weights and
+// returns, on lane r < topk, the r-th selected id (the caller stores the ids).
+// Each selected lane recomputes its expert's score (the same function, so the
+// same bits) rather than fetching it from the owner lane every round.
 template <int NS>
 __device__ __forceinline__ int kimi_select_token(const float* __restrict__ logits,
                                                  const float* __restrict__ bias,
-                                                 float* __restrict__ topk_weight,
-                                                 int32_t* __restrict__ topk_idx, int t,
+                                                 float* __restrict__ topk_weight, int t,
                                                  int n_experts, int topk, float route_scale) {
   const int lane = threadIdx.x & 63;
-  float score[NS];
+  const float* row = logits + static_cast<long long>(t) * n_experts;
   uint32_t key[NS];
 #pragma unroll
   for (int j = 0; j < NS; ++j) {
     const int e = lane + 64 * j;
-    if (e < n_experts) {
-      const float l = logits[static_cast<long long>(t) * n_experts + e];
-      score[j] = 1.0f / (1.0f + exp_exact_f32(-l));
-      key[j] = order_key(score[j] + bias[e]);
-    } else {
-      score[j] = 0.0f;
-      key[j] = 0;
-    }
+    key[j] = e < n_experts ? order_key(kimi_score(row[e]) + bias[e]) : 0u;
   }
+  const int my_i = wave_topk_ids<NS>(key, lane, topk);
+  const float my_s = lane < topk ? kimi_score(row[my_i]) : 0.0f;
+  // sum in selection order, as the reference's rounds add them
   float sum = 0.0f;
-  float my_w = 0.0f;  // lane r keeps selection r
-  int my_i = 0;
-  for (int r = 0; r < topk; ++r) {
-    const int sel = wave_argmax<NS>(key, lane);
-    const int owner = sel & 63, slot = sel >> 6;
-    const float s = lane_value(slot_value<NS>(score, slot), owner);
-    if (lane == owner) {
-#pragma unroll
-      for (int j = 0; j < NS; ++j)
-        if (j == slot) key[j] = 0;
-    }
-    if (lane == r) { my_w = s; my_i = sel; }
-    sum += s;
-  }
+  for (int r = 0; r < topk; ++r) sum += lane_value(my_s, r);
   const float scale = sum > 0.0f ? route_scale / sum : 0.0f;
-  if (lane < topk) {
-    topk_idx[t * topk + lane] = my_i;
-    topk_weight[t * topk + lane] = my_w * scale;
-  }
+  if (lane < topk) topk_weight[t * topk + lane] = my_s * scale;
   return my_i;
 }
 
@@ -145,53 +147,21 @@ __global__ void kimi_router_select_kernel(const float* __restrict__ logits,
                                           int n_experts, int topk, float route_scale) {
   const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (t >= tokens) return;  // whole waves leave
-  kimi_select_token<NS>(logits, bias, topk_weight, topk_idx, t, n_experts, topk, route_scale);
+  const int sel = kimi_select_token<NS>(logits, bias, topk_weight, t, n_experts, topk,
+                                        route_scale);
+  if ((threadIdx.x & 63) < topk) topk_idx[t * topk + (threadIdx.x & 63)] = sel;
 }
 
-// The router's select stage and the token -> expert permutation in one
-// workgroup (decode batches): the 16 waves select tokens t, t + 16, ...,
-// keep the ids in LDS, and the workgroup then runs the permutation's counting
-// sort on them (align_core.h), so the ids make no round trip through memory
-// and the pair costs one launch.  Outputs are those of the select kernel
-// followed by the permutation kernel, bit for bit.
+// DeepSeek-V2-Lite selection of token t by one wave: softmax (max-subtracted,
+// e^x rounded from a double exp, sum over experts 0, 1, 2, ... in order,
+// divide), top-k by probability (equal to the lower id), then ordered by
+// expert id.  Writes the weights; returns on lane r < topk the id of rank r
+// in id order (lanes >= topk return 0x7fffffff).
 template <int NS>
-__global__ __launch_bounds__(kAlignThreads) void kimi_route_align_kernel(
-    const float* __restrict__ logits, const float* __restrict__ bias,
-    float* __restrict__ topk_weight, int32_t* __restrict__ topk_idx,
-    int32_t* __restrict__ sorted_token_ids, int32_t* __restrict__ expert_ids,
-    int32_t* __restrict__ num_tokens_post_padded, uint32_t* __restrict__ expert_offsets,
-    uint32_t* __restrict__ expert_cursor, int tokens, int n_experts, int topk,
-    float route_scale, int global_start, int local_experts, int block_size,
-    int max_padded_tokens, int max_m_blocks) {
-  extern __shared__ __align__(16) unsigned char lds[];
-  const int route_elems = tokens * topk;
-  int32_t* s_idx = reinterpret_cast<int32_t*>(lds);  // [route_elems]
-  unsigned char* sort_lds = lds + ((route_elems * 4 + 15) & ~15);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  for (int t = wave; t < tokens; t += kAlignWaves) {
-    const int sel = kimi_select_token<NS>(logits, bias, topk_weight, topk_idx, t, n_experts,
-                                          topk, route_scale);
-    if (lane < topk) s_idx[t * topk + lane] = sel;
-  }
-  __syncthreads();
-  auto expert_of = [&](int r) {
-    if (r >= route_elems) return -1;
-    const int e = s_idx[r] - global_start;
-    return (e >= 0 && e < local_experts) ? e : -1;
-  };
-  align_workgroup(expert_of, sort_lds, sorted_token_ids, expert_ids, num_tokens_post_padded,
-                  expert_offsets, expert_cursor, route_elems, local_experts, block_size,
-                  max_padded_tokens, max_m_blocks);
-}
-
-template <int NS>
-__global__ void dsv2_router_select_kernel(const float* __restrict__ logits,
-                                          float* __restrict__ topk_weight,
-                                          int32_t* __restrict__ topk_idx, int tokens,
-                                          int n_experts, int topk) {
+__device__ __forceinline__ int dsv2_select_token(const float* __restrict__ logits,
+                                                 float* __restrict__ topk_weight, int t,
+                                                 int n_experts, int topk) {
   const int lane = threadIdx.x & 63;
-  const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  if (t >= tokens) return;  // whole waves leave
   float p[NS];
   uint32_t mkey = 0;
 #pragma unroll
@@ -204,7 +174,7 @@ __global__ void dsv2_router_select_kernel(const float* __restrict__ logits,
   const float mx = __builtin_bit_cast(float, (mkey & 0x80000000u) ? (mkey & 0x7fffffffu) : ~mkey);
 #pragma unroll
   for (int j = 0; j < NS; ++j)
-    p[j] = (lane + 64 * j < n_experts) ? exp_exact_f32(p[j] - mx) : 0.0f;
+    p[j] = (lane + 64 * j < n_experts) ? exp_exact_f32_fast(p[j] - mx) : 0.0f;
   // Sequential fp32 sum over experts 0, 1, 2, ... (the reference's order).
   float sum = 0.0f;
 #pragma unroll
@@ -216,28 +186,114 @@ __global__ void dsv2_router_select_kernel(const float* __restrict__ logits,
     p[j] = sum == 0.0f ? 0.0f : p[j] / sum;
     key[j] = lane + 64 * j < n_experts ? order_key(p[j]) : 0;
   }
-  int my_i = 0x7fffffff;  // lane r keeps selection r
+  const int sel = wave_topk_ids<NS>(key, lane, topk);
+  const int my_i = lane < topk ? sel : 0x7fffffff;
+  // the selected probability, from its owner lane's slot
   float my_w = 0.0f;
-  for (int r = 0; r < topk; ++r) {
-    const int sel = wave_argmax<NS>(key, lane);
-    const int owner = sel & 63, slot = sel >> 6;
-    const float w = lane_value(slot_value<NS>(p, slot), owner);
-    if (lane == owner) {
 #pragma unroll
-      for (int j = 0; j < NS; ++j)
-        if (j == slot) key[j] = 0;
-    }
-    if (lane == r) { my_i = sel; my_w = w; }
+  for (int j = 0; j < NS; ++j) {
+    const float v = __builtin_bit_cast(
+        float, __builtin_amdgcn_ds_bpermute((my_i & 63) << 2, __builtin_bit_cast(int, p[j])));
+    if (j == (my_i >> 6)) my_w = v;
   }
   // Order the selection by expert id: a lane's rank is the number of selected
   // ids below its own (selected ids are distinct).
   int rank = 0;
   for (int r = 0; r < topk; ++r)
     rank += __builtin_amdgcn_readlane(my_i, r) < my_i ? 1 : 0;
-  if (lane < topk) {
-    topk_idx[t * topk + rank] = my_i;
-    topk_weight[t * topk + rank] = my_w;
+  if (lane < topk) topk_weight[t * topk + rank] = my_w;
+  // hand rank r's id to lane r
+  int by_rank = 0x7fffffff;
+  for (int r = 0; r < topk; ++r) {
+    const int rr = __builtin_amdgcn_readlane(rank, r);
+    const int id = __builtin_amdgcn_readlane(my_i, r);
+    if (lane == rr) by_rank = id;
   }
+  return by_rank;
+}
+
+template <int NS>
+__global__ void dsv2_router_select_kernel(const float* __restrict__ logits,
+                                          float* __restrict__ topk_weight,
+                                          int32_t* __restrict__ topk_idx, int tokens,
+                                          int n_experts, int topk) {
+  const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (t >= tokens) return;  // whole waves leave
+  const int id = dsv2_select_token<NS>(logits, topk_weight, t, n_experts, topk);
+  if ((threadIdx.x & 63) < topk) topk_idx[t * topk + (threadIdx.x & 63)] = id;
+}
+
+// Arrivals of the fused router + permutation kernel's workgroups, per device.
+// Zero between launches: the last workgroup of a launch resets it.  Launches
+// that overlap on one device race on it.
+__device__ uint32_t g_route_arrivals;
+
+// The router's select stage and the token -> expert permutation in one launch.
+// Workgroup b's wave w selects tokens b + G (w + 16 i) (G = gridDim.x) and
+// stores their ids with device-scope atomic stores; the workgroup then counts
+// itself in on g_route_arrivals.  The last workgroup to arrive loads every id
+// with device-scope atomic loads, resets the counter and runs the
+// permutation's counting sort (align_core.h).  No workgroup waits for another,
+// and no device-wide fence is needed: the ids themselves are device-coherent
+// (the L2 is per XCD; an agent-scope release would write the whole L2 back),
+// and each workgroup's id stores are complete (s_waitcnt 0, then a barrier)
+// before its arrival is counted.  With one workgroup the ids go through LDS
+// only.  Outputs are those of the select kernel followed by the permutation
+// kernel, bit for bit.
+template <int NS, bool kDsv2>
+__global__ __launch_bounds__(kAlignThreads) void route_align_kernel(
+    const float* __restrict__ logits, const float* __restrict__ bias,
+    float* __restrict__ topk_weight, int32_t* topk_idx,
+    int32_t* __restrict__ sorted_token_ids, int32_t* __restrict__ expert_ids,
+    int32_t* __restrict__ num_tokens_post_padded, uint32_t* __restrict__ expert_offsets,
+    uint32_t* __restrict__ expert_cursor, int tokens, int n_experts, int topk,
+    float route_scale, int global_start, int local_experts, int block_size,
+    int max_padded_tokens, int max_m_blocks) {
+  extern __shared__ __align__(16) unsigned char lds[];
+  __shared__ int s_last;
+  const int route_elems = tokens * topk;
+  int32_t* s_idx = reinterpret_cast<int32_t*>(lds);  // [route_elems]
+  unsigned char* sort_lds = lds + ((route_elems * 4 + 15) & ~15);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int G = gridDim.x;
+  for (int t = blockIdx.x + G * wave; t < tokens; t += G * kAlignWaves) {
+    int sel;
+    if constexpr (kDsv2) sel = dsv2_select_token<NS>(logits, topk_weight, t, n_experts, topk);
+    else sel = kimi_select_token<NS>(logits, bias, topk_weight, t, n_experts, topk, route_scale);
+    if (lane < topk) {
+      if (G == 1) {
+        s_idx[t * topk + lane] = sel;
+        topk_idx[t * topk + lane] = sel;
+      } else {
+        __hip_atomic_store(&topk_idx[t * topk + lane], sel, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+  if (G > 1) {
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's id stores have completed
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const uint32_t prev = __hip_atomic_fetch_add(&g_route_arrivals, 1u, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+      s_last = prev == static_cast<uint32_t>(G - 1);
+      if (s_last)
+        __hip_atomic_store(&g_route_arrivals, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!s_last) return;
+    for (int r = threadIdx.x; r < route_elems; r += kAlignThreads)
+      s_idx[r] = __hip_atomic_load(&topk_idx[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  auto expert_of = [&](int r) {
+    if (r >= route_elems) return -1;
+    const int e = s_idx[r] - global_start;
+    return (e >= 0 && e < local_experts) ? e : -1;
+  };
+  align_workgroup(expert_of, sort_lds, sorted_token_ids, expert_ids, num_tokens_post_padded,
+                  expert_offsets, expert_cursor, route_elems, local_experts, block_size,
+                  max_padded_tokens, max_m_blocks);
 }
 
 constexpr int kWavesPerBlock = 4;
@@ -264,19 +320,31 @@ struct KimiLaunch {
   }
 };
 
-template <int NS>
-struct RouteAlignLaunch {
-  static void run(size_t lds, hipStream_t stream, const float* logits, const float* bias,
-                  float* w, int32_t* idx, int32_t* sorted_token_ids, int32_t* expert_ids,
-                  int32_t* ntp, uint32_t* expert_offsets, uint32_t* expert_cursor, int tokens,
-                  int n_experts, int topk, float scale, int global_start, int local_experts,
-                  int block_size, int max_padded_tokens, int max_m_blocks) {
-    hipLaunchKernelGGL(kimi_route_align_kernel<NS>, dim3(1), dim3(kAlignThreads), lds, stream,
-                       logits, bias, w, idx, sorted_token_ids, expert_ids, ntp, expert_offsets,
-                       expert_cursor, tokens, n_experts, topk, scale, global_start,
-                       local_experts, block_size, max_padded_tokens, max_m_blocks);
-  }
+// Workgroups of the fused router + permutation: about four tokens each (one
+// per SIMD), a single workgroup (ids through LDS only) up to four tokens.
+inline int route_align_grid(int tokens) { return tokens <= 4 ? 1 : ceil_div(tokens, 4); }
+
+template <bool kDsv2>
+struct RouteAlignLaunchT {
+  template <int NS>
+  struct L {
+    static void run(size_t lds, hipStream_t stream, const float* logits, const float* bias,
+                    float* w, int32_t* idx, int32_t* sorted_token_ids, int32_t* expert_ids,
+                    int32_t* ntp, uint32_t* expert_offsets, uint32_t* expert_cursor, int tokens,
+                    int n_experts, int topk, float scale, int global_start, int local_experts,
+                    int block_size, int max_padded_tokens, int max_m_blocks) {
+      hipLaunchKernelGGL((route_align_kernel<NS, kDsv2>), dim3(route_align_grid(tokens)),
+                         dim3(kAlignThreads), lds, stream, logits, bias, w, idx,
+                         sorted_token_ids, expert_ids, ntp, expert_offsets, expert_cursor,
+                         tokens, n_experts, topk, scale, global_start, local_experts,
+                         block_size, max_padded_tokens, max_m_blocks);
+    }
+  };
 };
+template <int NS>
+using KimiRouteAlignLaunch = RouteAlignLaunchT<false>::L<NS>;
+template <int NS>
+using Dsv2RouteAlignLaunch = RouteAlignLaunchT<true>::L<NS>;
 
 template <int NS>
 struct Dsv2Launch {
@@ -286,6 +354,41 @@ struct Dsv2Launch {
                        logits, w, idx, tokens, n_experts, topk);
   }
 };
+
+// Checks shared by the two fused router + permutation entry points; returns the
+// dynamic LDS size through *lds.
+int route_align_checks(const char* name, const float* logits, const void* bias,
+                       const float* topk_weight, const int32_t* topk_idx,
+                       const int32_t* sorted_token_ids, const int32_t* expert_ids,
+                       const int32_t* num_tokens_post_padded, const uint32_t* expert_offsets,
+                       const uint32_t* expert_cursor, int active_tokens, int n_experts,
+                       int topk, int global_start, int local_experts, int block_size,
+                       int max_padded_tokens, int max_m_blocks, size_t* lds) {
+  if (!logits || !bias || !topk_weight || !topk_idx || !sorted_token_ids || !expert_ids ||
+      !num_tokens_post_padded || !expert_offsets || !expert_cursor)
+    return fail(kInvalidValue, "%s: null pointer", name);
+  if (active_tokens <= 0 || n_experts <= 0 || n_experts > 64 * kMaxPerLane || topk <= 0 ||
+      topk > n_experts || topk > 64)
+    return fail(kInvalidValue, "%s: bad shape tokens=%d experts=%d topk=%d", name,
+                active_tokens, n_experts, topk);
+  if (global_start < 0 || local_experts <= 0 || local_experts > kAlignMaxExperts)
+    return fail(kInvalidValue, "%s: bad expert range start=%d E=%d", name, global_start,
+                local_experts);
+  if (!(block_size == 8 || (block_size >= 16 && block_size <= 64 && block_size % 16 == 0)))
+    return fail(kInvalidValue, "%s: block_size %d not in {8,16,32,48,64}", name, block_size);
+  const long long route_elems = static_cast<long long>(active_tokens) * topk;
+  if (route_elems > kRouteAlignMaxRoutes)
+    return fail(kNotSupported, "%s: %lld routes (at most %d in one workgroup)", name,
+                route_elems, kRouteAlignMaxRoutes);
+  const long long req_padded = route_elems + static_cast<long long>(local_experts) * (block_size - 1);
+  const int required_blocks = ceil_div(static_cast<int>(req_padded), block_size);
+  if (max_padded_tokens < req_padded || max_m_blocks < required_blocks)
+    return fail(kInvalidValue, "%s: capacity too small (padded %d < %lld or blocks %d < %d)",
+                name, max_padded_tokens, req_padded, max_m_blocks, required_blocks);
+  *lds = ((static_cast<size_t>(route_elems) * 4 + 15) & ~static_cast<size_t>(15)) +
+         align_lds_bytes(local_experts);
+  return kSuccess;
+}
 
 }  // namespace
 }  // namespace pega
@@ -312,9 +415,9 @@ PEGA_API int pega_kimi_router_select(const float* logits, const float* e_score_c
   return launch_status("kimi_router_select");
 }
 
-// The select stage and the token -> expert permutation in one launch of one
-// workgroup (no reference counterpart as one symbol: kimi_router.cu:20-91
-// followed by kimi_experts.cu:197-268).  Same outputs, bit for bit, as
+// The select stage and the token -> expert permutation in one launch (no
+// reference counterpart as one symbol: kimi_router.cu:20-91 followed by
+// kimi_experts.cu:197-268).  Same outputs, bit for bit, as
 // pega_kimi_router_select followed by pega_moe_align_block_size, with the
 // union of their argument checks; at most kRouteAlignMaxRoutes routes (decode
 // batches), kNotSupported above.
@@ -326,37 +429,47 @@ PEGA_API int pega_kimi_route_align(const float* logits, const float* e_score_cor
                                    int topk, float route_scale, int global_start,
                                    int local_experts, int block_size, int max_padded_tokens,
                                    int max_m_blocks, hipStream_t stream) {
-  if (!logits || !e_score_correction_bias || !topk_weight || !topk_idx || !sorted_token_ids ||
-      !expert_ids || !num_tokens_post_padded || !expert_offsets || !expert_cursor)
-    return fail(kInvalidValue, "kimi_route_align: null pointer");
-  if (active_tokens <= 0 || n_experts <= 0 || n_experts > 64 * kMaxPerLane || topk <= 0 ||
-      topk > n_experts || topk > 64 || !(route_scale > 0.0f))
-    return fail(kInvalidValue, "kimi_route_align: bad shape tokens=%d experts=%d topk=%d",
-                active_tokens, n_experts, topk);
-  if (global_start < 0 || local_experts <= 0 || local_experts > kAlignMaxExperts)
-    return fail(kInvalidValue, "kimi_route_align: bad expert range start=%d E=%d", global_start,
-                local_experts);
-  if (!(block_size == 8 || (block_size >= 16 && block_size <= 64 && block_size % 16 == 0)))
-    return fail(kInvalidValue, "kimi_route_align: block_size %d not in {8,16,32,48,64}",
-                block_size);
-  const long long route_elems = static_cast<long long>(active_tokens) * topk;
-  if (route_elems > kRouteAlignMaxRoutes)
-    return fail(kNotSupported, "kimi_route_align: %lld routes (at most %d in one workgroup)",
-                route_elems, kRouteAlignMaxRoutes);
-  const long long req_padded = route_elems + static_cast<long long>(local_experts) * (block_size - 1);
-  const int required_blocks = ceil_div(static_cast<int>(req_padded), block_size);
-  if (max_padded_tokens < req_padded || max_m_blocks < required_blocks)
-    return fail(kInvalidValue,
-                "kimi_route_align: capacity too small (padded %d < %lld or blocks %d < %d)",
-                max_padded_tokens, req_padded, max_m_blocks, required_blocks);
-  const size_t lds = ((static_cast<size_t>(route_elems) * 4 + 15) & ~static_cast<size_t>(15)) +
-                     align_lds_bytes(local_experts);
-  launch_slots<RouteAlignLaunch>(n_experts, lds, stream, logits, e_score_correction_bias,
-                                 topk_weight, topk_idx, sorted_token_ids, expert_ids,
-                                 num_tokens_post_padded, expert_offsets, expert_cursor,
-                                 active_tokens, n_experts, topk, route_scale, global_start,
-                                 local_experts, block_size, max_padded_tokens, max_m_blocks);
+  size_t lds = 0;
+  int rc = pega::route_align_checks("kimi_route_align", logits, e_score_correction_bias,
+                                    topk_weight, topk_idx, sorted_token_ids, expert_ids,
+                                    num_tokens_post_padded, expert_offsets, expert_cursor,
+                                    active_tokens, n_experts, topk, global_start, local_experts,
+                                    block_size, max_padded_tokens, max_m_blocks, &lds);
+  if (rc != kSuccess) return rc;
+  if (!(route_scale > 0.0f))
+    return fail(kInvalidValue, "kimi_route_align: route_scale must be positive");
+  launch_slots<KimiRouteAlignLaunch>(n_experts, lds, stream, logits, e_score_correction_bias,
+                                     topk_weight, topk_idx, sorted_token_ids, expert_ids,
+                                     num_tokens_post_padded, expert_offsets, expert_cursor,
+                                     active_tokens, n_experts, topk, route_scale, global_start,
+                                     local_experts, block_size, max_padded_tokens, max_m_blocks);
   return launch_status("kimi_route_align");
+}
+
+// The DeepSeek-V2-Lite router (softmax top-k ordered by expert id) and the
+// token -> expert permutation in one launch (no reference counterpart as one
+// symbol: host_ops.rs:388-412 / dsv2_lite_moe.cu:41-129 followed by the
+// permutation).  Same outputs, bit for bit, as pega_dsv2_router_select
+// followed by pega_moe_align_block_size.
+PEGA_API int pega_dsv2_route_align(const float* logits, float* topk_weight, int32_t* topk_idx,
+                                   int32_t* sorted_token_ids, int32_t* expert_ids,
+                                   int32_t* num_tokens_post_padded, uint32_t* expert_offsets,
+                                   uint32_t* expert_cursor, int tokens, int n_experts, int topk,
+                                   int global_start, int local_experts, int block_size,
+                                   int max_padded_tokens, int max_m_blocks, hipStream_t stream) {
+  size_t lds = 0;
+  int rc = pega::route_align_checks("dsv2_route_align", logits, logits, topk_weight, topk_idx,
+                                    sorted_token_ids, expert_ids, num_tokens_post_padded,
+                                    expert_offsets, expert_cursor, tokens, n_experts, topk,
+                                    global_start, local_experts, block_size, max_padded_tokens,
+                                    max_m_blocks, &lds);
+  if (rc != kSuccess) return rc;
+  launch_slots<Dsv2RouteAlignLaunch>(n_experts, lds, stream, logits, nullptr, topk_weight,
+                                     topk_idx, sorted_token_ids, expert_ids,
+                                     num_tokens_post_padded, expert_offsets, expert_cursor,
+                                     tokens, n_experts, topk, 1.0f, global_start, local_experts,
+                                     block_size, max_padded_tokens, max_m_blocks);
+  return launch_status("dsv2_route_align");
 }
 
 // DeepSeek-V2-Lite softmax top-k (no reference C symbol: the reference runs

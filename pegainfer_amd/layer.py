@@ -148,6 +148,28 @@ class RoutedExperts:
         return ops.kimi_route_align(self.route_ws, logits, bias, topk_w, topk_idx, T,
                                     self.global_start, route_scale)
 
+    def route_softmax_from_logits(self, logits: torch.Tensor, topk_w: torch.Tensor,
+                                  topk_idx: torch.Tensor, T: int):
+        """DeepSeek-V2-Lite router + permutation in one launch (ops.dsv2_route_align);
+        returns the routing to pass to forward."""
+        return ops.dsv2_route_align(self.route_ws, logits, topk_w, topk_idx, T, self.global_start)
+
+    def forward_from_logits(self, hidden: torch.Tensor, logits: torch.Tensor, bias: torch.Tensor,
+                            topk_w: torch.Tensor, topk_idx: torch.Tensor, out_f32: torch.Tensor,
+                            route_scale: float = 1.0, **kw) -> torch.Tensor:
+        """The Kimi router's select stage, then forward: in one fused select +
+        permutation launch up to ops.ROUTE_ALIGN_MAX_ROUTES routes (same bits as the
+        select and permutation launches, which run above that)."""
+        T = hidden.shape[0]
+        routing = None
+        if fused_route(T, self.topk, logits.shape[-1]):
+            routing = self.route_from_logits(logits, bias, topk_w[:T], topk_idx[:T], T,
+                                             route_scale)
+        else:
+            ops.kimi_router_select(logits, bias, topk_w[:T], topk_idx[:T], T, topk=self.topk,
+                                   route_scale=route_scale)
+        return self.forward(hidden, topk_idx[:T], topk_w[:T], out_f32, routing=routing, **kw)
+
 
 class DenseW4A16:
     """y = x . dequant(W)^T for one W4A16 matrix (a one-expert grouped GEMM with
@@ -207,11 +229,16 @@ class KimiSharedExpert:
         return projected
 
 
-# Token counts up to which the decode layer routes with the fused select +
-# permutation launch: measured 9.2 against 9.9 µs (T = 1) and 9.5 against 10.0 µs
-# (T = 4) for the pair of launches; from 16 tokens one workgroup selecting the
-# tokens in turn is slower (11.8 against 10.5 µs; 31 against 11 µs at 64).
-FUSED_ROUTE_MAX_TOKENS = 4
+def fused_route(tokens: int, topk: int, n_experts: int, softmax: bool = False) -> bool:
+    """Whether a layer routes with the fused select + permutation launch.  Kimi
+    (sigmoid): whenever its routes fit the one-workgroup sort (ops.ROUTE_ALIGN_MAX_ROUTES)
+    and the expert count fits the select (at most 1024); graph-timed against the select
+    and permutation launches: 9.1 / 10.3 / 11.8 / 12.0 against 9.9 / 11.2 / 12.0 / 12.3 us
+    at 1 / 4 / 16 / 64 tokens.  DeepSeek-V2-Lite (softmax): up to 512 routes; at C4's
+    512 tokens (3072 routes) the fused launch took 14.9 against 13.9 us, its 128
+    workgroups' hand-off costing more than the second launch."""
+    limit = 512 if softmax else ops.ROUTE_ALIGN_MAX_ROUTES
+    return tokens * topk <= limit and n_experts <= 1024
 
 
 class KimiMoeDecodeLayer:
@@ -234,16 +261,8 @@ class KimiMoeDecodeLayer:
         T = hidden.shape[0]
         projected, routed_f32 = self.projected[:T], self.routed_f32[:T]
         self.shared.forward(normed, projected)
-        routing = None
-        if T <= FUSED_ROUTE_MAX_TOKENS and logits.shape[-1] == 384:
-            # select + permutation in one launch (same bits as the two launches)
-            routing = self.routed.route_from_logits(logits, bias, self.topk_w[:T],
-                                                    self.topk_idx[:T], T)
-        else:
-            ops.kimi_router_select(logits, bias, self.topk_w[:T], self.topk_idx[:T], T,
-                                   topk=self.routed.topk)
-        self.routed.forward(normed, self.topk_idx[:T], self.topk_w[:T], routed_f32,
-                            routing=routing)
+        self.routed.forward_from_logits(normed, logits, bias, self.topk_w, self.topk_idx,
+                                        routed_f32)
         ops.kimi_residual_add_scaled_f32(hidden, projected, routed_f32, ops.KIMI_K2_ROUTER_SCALE,
                                          out)
         return out
@@ -316,6 +335,15 @@ class Dsv2MoeLayer:
         self.side = None
         self.device = device
 
+    def _route(self, logits: torch.Tensor, T: int):
+        """Softmax top-k select and permutation: one fused launch where the routes fit it
+        (then the routing goes to forward), else the select launch (forward permutes)."""
+        if fused_route(T, self.routed.topk, logits.shape[-1], softmax=True):
+            return self.routed.route_softmax_from_logits(logits, self.topk_w[:T],
+                                                         self.topk_idx[:T], T)
+        ops.dsv2_router_select(logits, self.topk_w[:T], self.topk_idx[:T], T, self.routed.topk)
+        return None
+
     def forward(self, hidden: torch.Tensor, logits: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
         """The shared expert does not depend on the routed branch, so by default it
         overlaps with it: its few large workgroups (one expert, 512 rows) share the
@@ -327,10 +355,9 @@ class Dsv2MoeLayer:
         T = hidden.shape[0]
         if self.pair:
             companion = self.shared.pair_problems(hidden, self.shared_out[:T])
-            ops.dsv2_router_select(logits, self.topk_w[:T], self.topk_idx[:T], T,
-                                   self.routed.topk)
+            routing = self._route(logits, T)
             self.routed.forward(hidden, self.topk_idx[:T], self.topk_w[:T], self.routed_f32[:T],
-                                combine="weighted", companion=companion)
+                                combine="weighted", companion=companion, routing=routing)
             ops.moe_join_routed_shared(self.routed_f32[:T], self.shared_out[:T], out)
             return out
         main = torch.cuda.current_stream()
@@ -340,9 +367,9 @@ class Dsv2MoeLayer:
             self.side.wait_stream(main)
             with torch.cuda.stream(self.side):
                 self.shared.forward(hidden, self.shared_out[:T])
-        ops.dsv2_router_select(logits, self.topk_w[:T], self.topk_idx[:T], T, self.routed.topk)
+        routing = self._route(logits, T)
         self.routed.forward(hidden, self.topk_idx[:T], self.topk_w[:T], self.routed_f32[:T],
-                            combine="weighted")
+                            combine="weighted", routing=routing)
         if self.side is not None:
             main.wait_stream(self.side)
         else:

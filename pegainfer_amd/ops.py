@@ -701,6 +701,36 @@ def kimi_route_align(workspace: KimiMarlinRouteWorkspace, logits: torch.Tensor, 
                              ws.num_tokens_post_padded)
 
 
+def dsv2_route_align(workspace: KimiMarlinRouteWorkspace, logits: torch.Tensor,
+                     topk_weight: torch.Tensor, topk_idx: torch.Tensor, tokens: int,
+                     global_expert_start: int) -> KimiMarlinRouting:
+    """The DeepSeek-V2-Lite router (softmax top-k ordered by expert id) and the
+    token -> expert permutation in one launch (pega_dsv2_route_align): the outputs of
+    dsv2_router_select followed by moe_align_block_size, bit for bit (at most 4096
+    routes)."""
+    ws = workspace
+    n_experts = logits.shape[-1]
+    _ensure(tokens > 0, "tokens must be positive")
+    _ensure_router_inputs(logits, None, tokens, n_experts)
+    _ensure(tokens <= ws.max_active_tokens,
+            f"tokens {tokens} exceed the route workspace capacity {ws.max_active_tokens}")
+    route_elems = tokens * ws.topk
+    _ensure(route_elems <= ROUTE_ALIGN_MAX_ROUTES,
+            f"{route_elems} routes exceed the fused select + permutation's {ROUTE_ALIGN_MAX_ROUTES}")
+    _ensure(topk_idx.dtype == torch.int32 and topk_idx.numel() >= route_elems,
+            "topk_idx must be int32 covering tokens * topk")
+    _ensure(topk_weight.dtype == torch.float32 and topk_weight.numel() >= route_elems,
+            "topk_weight must be f32 covering tokens * topk")
+    _lib.call("pega_dsv2_route_align", _ptr(logits), _ptr(topk_weight), _ptr(topk_idx),
+              _ptr(ws.sorted_token_ids), _ptr(ws.expert_ids), _ptr(ws.num_tokens_post_padded),
+              _ptr(ws.expert_offsets), _ptr(ws.expert_cursor), tokens, n_experts, ws.topk,
+              global_expert_start, ws.local_experts, ws.block_size, ws.max_padded_tokens,
+              ws.max_m_blocks, _stream())
+    return KimiMarlinRouting(tokens, tokens, route_elems, global_expert_start, ws.block_size,
+                             ws.max_padded_tokens, ws.max_m_blocks, ws.topk, ws.local_experts,
+                             ws.sorted_token_ids, ws.expert_ids, ws.num_tokens_post_padded)
+
+
 def kimi_router_select(logits: torch.Tensor, bias: torch.Tensor, topk_weight: torch.Tensor,
                        topk_idx: torch.Tensor, active_tokens: int, topk: int = KIMI_K2_TOPK,
                        route_scale: float = 1.0) -> None:

@@ -73,14 +73,15 @@ def test_dense_gemm_entry_points_agree_and_reject(oracle):
     assert L.gemm_graphsafe_cuda(p(w), p(x), p(y2), M, 0, K, s) == 1
 
 
-@pytest.mark.parametrize("T", [24, 3])
+@pytest.mark.parametrize("T", [24, 3, 600])
 def test_kimi_decode_layer_with_shared_expert(oracle, T):
     """Shared expert (bf16 gate/up and down), router select, routed experts and
     the residual join, against the oracle's chain of the same stages.  At 3 tokens
-    the layer routes through the fused select + permutation launch."""
+    the layer routes through the fused select + permutation launch in one workgroup,
+    at 24 in several, and at 600 (4800 routes) through the two launches."""
     from pegainfer_amd import layer, ops, synth
     E, H, I, SI = 48, 1024, 256, 512
-    assert (T <= layer.FUSED_ROUTE_MAX_TOKENS) == (T == 3)
+    assert layer.fused_route(T, 8, 384) == (T != 600)
     g = synth.rng(11, T)
     gate, up, down = (synth.int4_checkpoint(g, E, I, H), synth.int4_checkpoint(g, E, I, H),
                       synth.int4_checkpoint(g, E, H, I))
@@ -106,9 +107,15 @@ def test_kimi_decode_layer_with_shared_expert(oracle, T):
     routed_ref, _ = oracle.kimi_moe_layer(normed, w13p, w13s, down[0], down[1], idx.reshape(-1),
                                           w, global_start=0, local_experts=E,
                                           block_size=routed.block_size, hidden=H, inter=I)
-    ref = oracle.residual_add_scaled_f32(hidden, proj, routed_ref, ops.KIMI_K2_ROUTER_SCALE)
-    # two GEMM chains of the same tolerance composed: twice the per-GEMM bound
-    assert_bf16_close(host(out), ref, rtol=2e-2, atol=2e-3, what="Kimi decode layer")
+    # the routed branch against the oracle's fp32 layer output, at the routed-layer bound
+    rg, rr = host(moe.routed_f32).astype(np.float64), routed_ref.astype(np.float64)
+    assert (np.abs(rg - rr) <= 2e-3 + 2e-2 * np.abs(rr)).all(), "routed branch"
+    if T <= 24:
+        # two GEMM chains of the same tolerance composed: twice the per-GEMM bound (over
+        # 600 x 1024 outputs the routed error, scaled by 2.827 in the join, reaches that
+        # bound's tail near zero, so the larger case checks the stages instead)
+        ref = oracle.residual_add_scaled_f32(hidden, proj, routed_ref, ops.KIMI_K2_ROUTER_SCALE)
+        assert_bf16_close(host(out), ref, rtol=2e-2, atol=2e-3, what="Kimi decode layer")
     # the join itself is exact given its inputs
     assert np.array_equal(host(out), oracle.residual_add_scaled_f32(
         hidden, host(moe.projected), host(moe.routed_f32), ops.KIMI_K2_ROUTER_SCALE))

@@ -271,3 +271,106 @@ def test_kimi_route_align_rejections():
     base[0] = ctypes.c_void_p(0)
     assert call(4) == 1
 
+
+
+@pytest.mark.parametrize("tokens,bs,start,E,seed", [
+    (1, 8, 0, 64, 0), (4, 16, 0, 64, 1), (5, 16, 8, 48, 2), (64, 32, 0, 64, 3),
+    (512, 64, 0, 64, 4), (682, 64, 0, 64, 5), (100, 64, 16, 32, 6)])
+def test_dsv2_route_align_matches_two_launches(oracle, tokens, bs, start, E, seed):
+    """The fused DeepSeek-V2-Lite select + permutation against the select kernel followed
+    by the permutation kernel (64 experts, top-6), bit for bit, and the permutation against
+    the oracle; outputs past the active rows are left as they were."""
+    from pegainfer_amd import ops
+    g = np.random.default_rng(170 + seed)
+    logits = dev(g.standard_normal((tokens, 64)).astype(np.float32))
+    ws_a = ops.KimiMarlinRouteWorkspace(tokens + 3, bs, topk=6, local_experts=E)
+    ws_b = ops.KimiMarlinRouteWorkspace(tokens + 3, bs, topk=6, local_experts=E)
+    for ws in (ws_a, ws_b):
+        for t in (ws.sorted_token_ids, ws.expert_ids, ws.expert_offsets, ws.expert_cursor):
+            t.fill_(-7)
+    w_a = torch.full(((tokens + 3) * 6,), -1.0, dtype=torch.float32, device="cuda")
+    w_b = w_a.clone()
+    i_a = torch.full(((tokens + 3) * 6,), -3, dtype=torch.int32, device="cuda")
+    i_b = i_a.clone()
+    ops.dsv2_router_select(logits, w_a, i_a, tokens, 6)
+    ops.moe_align_block_size(ws_a, i_a, tokens, tokens, start)
+    ops.dsv2_route_align(ws_b, logits, w_b, i_b, tokens, start)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(i_a), host(i_b))
+    assert np.array_equal(host(w_a).view(np.uint32), host(w_b).view(np.uint32))
+    assert (host(i_b)[tokens * 6:] == -3).all() and (host(w_b)[tokens * 6:] == -1.0).all()
+    for name in ("sorted_token_ids", "expert_ids", "num_tokens_post_padded", "expert_offsets",
+                 "expert_cursor"):
+        assert np.array_equal(host(getattr(ws_a, name)), host(getattr(ws_b, name))), name
+    _check_against_oracle(oracle, ws_b, host(i_b)[:tokens * 6], start, E, bs)
+
+
+@pytest.mark.parametrize("tokens", [1, 4, 64, 512])
+def test_fused_route_align_against_the_oracle_routers(oracle, tokens):
+    """Both fused entry points straight against the CPU routers (oracle.kimi_router,
+    oracle.dsv2_router): ids and weights bit for bit, and the permutation of those ids."""
+    from pegainfer_amd import ops
+    g = np.random.default_rng(300 + tokens)
+    # Kimi: 384 experts, top-8, nonzero bias, 48 local experts from 96
+    logits = g.standard_normal((tokens, 384)).astype(np.float32)
+    bias = (g.standard_normal(384) * 0.03).astype(np.float32)
+    ws = ops.KimiMarlinRouteWorkspace(tokens, 16, topk=8, local_experts=48)
+    w = torch.zeros(tokens * 8, dtype=torch.float32, device="cuda")
+    i = torch.zeros(tokens * 8, dtype=torch.int32, device="cuda")
+    ops.kimi_route_align(ws, dev(logits), dev(bias), w, i, tokens, 96, route_scale=2.5)
+    ref_idx, ref_w = oracle.kimi_router(logits, bias, 8, 2.5)
+    assert np.array_equal(host(i).reshape(tokens, 8), ref_idx)
+    assert np.array_equal(host(w).reshape(tokens, 8).view(np.uint32), ref_w.view(np.uint32))
+    _check_against_oracle(oracle, ws, ref_idx.reshape(-1), 96, 48, 16)
+    # DeepSeek-V2-Lite: 64 experts, top-6 softmax, all local
+    logits = g.standard_normal((tokens, 64)).astype(np.float32)
+    if tokens >= 4:
+        logits[3] = load_golden("misc_kat.npz")["dsv2_logits"]
+    ws = ops.KimiMarlinRouteWorkspace(tokens, 64, topk=6, local_experts=64)
+    w = torch.zeros(tokens * 6, dtype=torch.float32, device="cuda")
+    i = torch.zeros(tokens * 6, dtype=torch.int32, device="cuda")
+    ops.dsv2_route_align(ws, dev(logits), w, i, tokens, 0)
+    ref_idx, ref_w = oracle.dsv2_router(logits, 6)
+    assert np.array_equal(host(i).reshape(tokens, 6), ref_idx)
+    assert np.array_equal(host(w).reshape(tokens, 6).view(np.uint32), ref_w.view(np.uint32))
+    if tokens >= 4:
+        assert list(ref_idx[3]) == [7, 10, 20, 41, 54, 58]
+    _check_against_oracle(oracle, ws, ref_idx.reshape(-1), 0, 64, 64)
+
+
+def test_fused_route_align_repeated_and_graph_replays():
+    """The multi-workgroup hand-off resets its arrival counter: calls in a row with
+    different token counts, then a captured call replayed with new logits copied in
+    between (eager work and synchronisation between replays), each equal to the two
+    launches."""
+    from pegainfer_amd import layer, ops
+    g = np.random.default_rng(5)
+    T = 64
+    logits = torch.zeros(T, 384, dtype=torch.float32, device="cuda")
+    bias = dev((g.standard_normal(384) * 0.02).astype(np.float32))
+    ws_a = ops.KimiMarlinRouteWorkspace(T, 16, topk=8, local_experts=48)
+    ws_b = ops.KimiMarlinRouteWorkspace(T, 16, topk=8, local_experts=48)
+    w_a = torch.zeros(T * 8, dtype=torch.float32, device="cuda")
+    i_a = torch.zeros(T * 8, dtype=torch.int32, device="cuda")
+    w_b, i_b = w_a.clone(), i_a.clone()
+
+    def compare(n):
+        ops.kimi_router_select(logits, bias, w_a, i_a, n)
+        ops.moe_align_block_size(ws_a, i_a, n, n, 0)
+        torch.cuda.synchronize()
+        assert np.array_equal(host(i_a)[:n * 8], host(i_b)[:n * 8])
+        assert np.array_equal(host(w_a)[:n * 8], host(w_b)[:n * 8])
+        for name in ("sorted_token_ids", "expert_ids", "num_tokens_post_padded",
+                     "expert_offsets", "expert_cursor"):
+            assert np.array_equal(host(getattr(ws_a, name)), host(getattr(ws_b, name))), name
+
+    for n in (64, 9, 64, 33, 5, 64):
+        logits.copy_(dev(g.standard_normal((T, 384)).astype(np.float32)))
+        ops.kimi_route_align(ws_b, logits, bias, w_b, i_b, n, 0)
+        compare(n)
+    graph = layer.capture_graph(lambda: ops.kimi_route_align(ws_b, logits, bias, w_b, i_b, T, 0))
+    for _ in range(3):
+        logits.copy_(dev(g.standard_normal((T, 384)).astype(np.float32)))
+        torch.cuda.synchronize()
+        graph.replay()
+        compare(T)
