@@ -73,14 +73,13 @@ def test_noalloc_first_call_inside_graph_capture_then_replays():
         assert np.array_equal(host(got), r)
 
 
-def _run_pair(E, T, topk, bs, inter, K, seed, workspace_floats=None):
-    """Both entries on the same problem; the workspace entry gets room for 16 shares (or
-    `workspace_floats`), so both pick the same share count (the static scratch holds at
-    least as many here)."""
+def _run_pair(E, T, topk, bs, inter, K, seed):
+    """Both entries on the same problem, the workspace entry with a workspace of the
+    static scratch's size: the documented equality (the share count depends on the
+    buffer's size)."""
     w13, x, routing = _problem(E, T, topk, bs, inter, K, seed)
     routes = T * topk
-    n = workspace_floats if workspace_floats is not None else 16 * routes * 2 * inter
-    partials = torch.zeros(n, dtype=torch.float32, device="cuda")
+    partials = torch.zeros(SCRATCH_FLOATS, dtype=torch.float32, device="cuda")
     ref = torch.full((routes, inter), float("nan"), dtype=torch.bfloat16, device="cuda")
     got = torch.full((routes, inter), float("nan"), dtype=torch.bfloat16, device="cuda")
     assert _call("workspace", routing, x, w13, ref, T, topk, inter, K, E, partials) == 0
@@ -101,11 +100,10 @@ def test_noalloc_matches_workspace_entry_twice_second_smaller():
 
 
 def test_noalloc_no_split_shape_and_scratch_limit():
-    # C3-like: many (block, tile) workgroups, no split, no scratch used
+    # C3-like: 77 capacity blocks x 8 column tiles, two workgroups per CU: no split
     _run_pair(E=48, T=64, topk=8, bs=16, inter=256, K=1024, seed=3)
-    # a split is wanted (14 capacity blocks x 32 tiles < 2 workgroups per CU) but two shares of
-    # 200 routes x 2048 columns exceed the 524,288-float scratch: it runs unsplit, with the
-    # bits the workspace entry gives with a workspace of the scratch's size
-    n = _run_pair(E=1, T=200, topk=1, bs=16, inter=1024, K=1024, seed=4,
-                  workspace_floats=SCRATCH_FLOATS)
+    # a split is wanted (14 capacity blocks x 32 tiles < 2 workgroups per CU) but two shares
+    # of 200 routes x 2048 columns exceed the 524,288-float scratch: it runs unsplit, as the
+    # workspace entry does with a workspace of the scratch's size
+    n = _run_pair(E=1, T=200, topk=1, bs=16, inter=1024, K=1024, seed=4)
     assert n == 200
