@@ -596,6 +596,35 @@ def bench_c5(torch, args, results):
     log(f"C5: R={routes}, layer {ms * 1e3:.1f} us ({results['c5']['tflops']:.1f} TFLOP/s), "
         f"W13+SwiGLU {w13_ms * 1e3:.1f} us ({results['c5']['w13_tflops']:.1f} TFLOP/s), "
         f"W2 {w2_ms * 1e3:.1f} us ({results['c5']['w2_tflops']:.1f} TFLOP/s)")
+    del moe
+    bench_c5_shared(torch, args, results, hidden)
+
+
+def bench_c5_shared(torch, args, results, normed):
+    """The Kimi shared expert (bf16 dense MLP, gate/up [4096, 7168], down [7168, 2048],
+    seeded N(0, 0.02) weights) on C5's 4096 prefill tokens: gate/up GEMM, SwiGLU, down
+    GEMM (the reference's prefill sequence, hipBLASLt GEMMs), against bf16 MFMA peak."""
+    from pegainfer_amd import layer, ops, synth
+    T, H, SI = normed.shape[0], 7168, 2048
+    g = synth.rng(5, 4)
+    gu = dev(torch, synth.normal_bf16(g, (2 * SI, H), std=0.02), bf16=True)
+    dn = dev(torch, synth.normal_bf16(g, (H, SI), std=0.02), bf16=True)
+    shared = layer.KimiSharedExpert(gu, dn, max_tokens=T)
+    proj = torch.zeros(T, H, dtype=torch.bfloat16, device="cuda")
+    steps = max(5, args.steps // 5)
+    ms = time_graph(torch, lambda: shared.forward(normed, proj), steps, 2, calls=4)
+    gu_ms = time_graph(torch, lambda: ops.gemm_graphsafe(gu, normed, shared.h13[:T]), steps, 2,
+                       calls=4)
+    flops = 2 * T * (2 * SI * H + H * SI)
+    gu_flops = 2 * T * 2 * SI * H
+    results["c5_shared"] = dict(
+        workload="c5_kimi_shared_expert_t4096", tokens=T, hidden=H, inter=SI,
+        launch="hip_graph (4 calls per graph)", us=ms * 1e3, flops=flops,
+        tflops=flops / (ms * 1e-3) / 1e12, frac_of_bf16_peak=flops / (ms * 1e-3) / 2.5e15,
+        gate_up_us=gu_ms * 1e3, gate_up_tflops=gu_flops / (gu_ms * 1e-3) / 1e12)
+    log(f"C5 shared expert (T={T}): MLP {ms * 1e3:.1f} us ({results['c5_shared']['tflops']:.0f} "
+        f"TFLOP/s, {results['c5_shared']['frac_of_bf16_peak']:.3f} of bf16 peak), gate/up GEMM "
+        f"{gu_ms * 1e3:.1f} us ({results['c5_shared']['gate_up_tflops']:.0f} TFLOP/s)")
 
 
 def load_traffic(name):

@@ -30,6 +30,12 @@
 // the same k slots per lane, so the product is exact whatever k order the
 // MFMA assigns to them.  Token rows past N read zeros through an
 // out-of-range buffer offset and are never stored.
+#include <hipblaslt/hipblaslt.h>
+
+#include <map>
+#include <mutex>
+#include <tuple>
+
 #include "common.h"
 #include "pega_moe.h"
 
@@ -294,6 +300,108 @@ int dense_launch(const uint16_t* W, const uint16_t* X, void* Y, int rows, int M,
   return launch_status(name);
 }
 
+// ---------------------------------------------------------------- prefill sizes
+// From kLtMinTokens tokens up the GEMM is compute-bound and a plain library
+// GEMM serves it: hipBLASLt's bf16 x bf16 -> bf16 kernel with fp32 accumulation
+// (the reference runs cuBLAS there: cublasGemmEx with CUBLAS_COMPUTE_32F,
+// linear.cu:321-344).  Column-major, as the reference states the call:
+// C (M x N, ld M) = op_T(W: K x M, ld K) . op_N(X: K x N, ld K).  No workspace
+// (an algorithm that needs none), so a call allocates nothing on the device; the
+// library handle and each shape's descriptors and algorithm are made on the
+// shape's first call on a device and reused.
+constexpr int kLtMinTokens = 256;
+
+struct LtPlan {
+  hipblasLtMatmulDesc_t desc = nullptr;
+  hipblasLtMatrixLayout_t a = nullptr, b = nullptr, c = nullptr;
+  hipblasLtMatmulAlgo_t algo{};
+};
+
+struct LtDevice {
+  std::mutex mu;
+  hipblasLtHandle_t handle = nullptr;
+  std::map<std::tuple<int, int, int>, LtPlan> plans;
+};
+LtDevice g_lt[64];
+
+int lt_plan(int dev, int M, int N, int K, const char* name, LtDevice** out_d, LtPlan* out) {
+  LtDevice& d = g_lt[dev];
+  std::lock_guard<std::mutex> lock(d.mu);
+  if (d.handle == nullptr && hipblasLtCreate(&d.handle) != HIPBLAS_STATUS_SUCCESS) {
+    d.handle = nullptr;
+    return fail(kLaunchFailed, "%s: hipblasLtCreate failed", name);
+  }
+  const auto key = std::make_tuple(M, N, K);
+  auto it = d.plans.find(key);
+  if (it == d.plans.end()) {
+    LtPlan pl;
+    const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
+    bool ok = hipblasLtMatmulDescCreate(&pl.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) ==
+                  HIPBLAS_STATUS_SUCCESS &&
+              hipblasLtMatmulDescSetAttribute(pl.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta,
+                                              sizeof(ta)) == HIPBLAS_STATUS_SUCCESS &&
+              hipblasLtMatmulDescSetAttribute(pl.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb,
+                                              sizeof(tb)) == HIPBLAS_STATUS_SUCCESS &&
+              hipblasLtMatrixLayoutCreate(&pl.a, HIP_R_16BF, K, M, K) == HIPBLAS_STATUS_SUCCESS &&
+              hipblasLtMatrixLayoutCreate(&pl.b, HIP_R_16BF, K, N, K) == HIPBLAS_STATUS_SUCCESS &&
+              hipblasLtMatrixLayoutCreate(&pl.c, HIP_R_16BF, M, N, M) == HIPBLAS_STATUS_SUCCESS;
+    hipblasLtMatmulPreference_t pref = nullptr;
+    hipblasLtMatmulHeuristicResult_t res[1];
+    int found = 0;
+    if (ok) {
+      const uint64_t ws = 0;
+      ok = hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS &&
+           hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES,
+                                                 &ws, sizeof(ws)) == HIPBLAS_STATUS_SUCCESS &&
+           hipblasLtMatmulAlgoGetHeuristic(d.handle, pl.desc, pl.a, pl.b, pl.c, pl.c, pref, 1,
+                                           res, &found) == HIPBLAS_STATUS_SUCCESS &&
+           found > 0 && res[0].workspaceSize == 0;
+    }
+    if (pref) hipblasLtMatmulPreferenceDestroy(pref);
+    if (!ok) {
+      if (pl.a) hipblasLtMatrixLayoutDestroy(pl.a);
+      if (pl.b) hipblasLtMatrixLayoutDestroy(pl.b);
+      if (pl.c) hipblasLtMatrixLayoutDestroy(pl.c);
+      if (pl.desc) hipblasLtMatmulDescDestroy(pl.desc);
+      return fail(kNotSupported, "%s: no hipBLASLt algorithm without workspace for M=%d N=%d K=%d",
+                  name, M, N, K);
+    }
+    pl.algo = res[0].algo;
+    it = d.plans.emplace(key, pl).first;
+  }
+  *out_d = &d;
+  *out = it->second;
+  return kSuccess;
+}
+
+int lt_gemm(const uint16_t* W, const uint16_t* X, uint16_t* Y, int M, int N, int K,
+            hipStream_t stream, const char* name) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+    return fail(kInvalidValue, "%s: no current device", name);
+  LtDevice* d = nullptr;
+  LtPlan pl;
+  const int rc = lt_plan(dev, M, N, K, name, &d, &pl);
+  if (rc != kSuccess) return rc;
+  const float alpha = 1.0f, beta = 0.0f;
+  const hipblasStatus_t st = hipblasLtMatmul(d->handle, pl.desc, &alpha, W, pl.a, X, pl.b, &beta,
+                                             Y, pl.c, Y, pl.c, &pl.algo, nullptr, 0, stream);
+  if (st != HIPBLAS_STATUS_SUCCESS) return fail(kLaunchFailed, "%s: hipblasLtMatmul failed", name);
+  return launch_status(name);
+}
+
+// gemm_cuda / gemm_graphsafe_cuda: the checks of dense_launch, then the token
+// count picks the kernel.
+int dense_gemm_bf16(const uint16_t* W, const uint16_t* X, uint16_t* Y, int M, int N, int K,
+                    hipStream_t stream, const char* name) {
+  if (N < kLtMinTokens || !W || !X || !Y || M <= 0 || N <= 0 || K <= 0 || M % 16 != 0 ||
+      K % 32 != 0 || (reinterpret_cast<uintptr_t>(W) & 15u) != 0 ||
+      (reinterpret_cast<uintptr_t>(X) & 15u) != 0 ||
+      static_cast<long long>(N) * K * 2 >= static_cast<long long>(kOutOfRange))
+    return dense_launch<false>(W, X, Y, M, M, N, K, stream, name);
+  return lt_gemm(W, X, Y, M, N, K, stream, name);
+}
+
 }  // namespace
 
 // The router's logits GEMM (fp32 output); declared in common.h.
@@ -307,16 +415,19 @@ int dense_gemm_f32(const uint16_t* W, const uint16_t* X, float* Y, int M, int N,
 using namespace pega;
 
 // Reference: pegainfer-kernels/src/ffi/shared.rs:220-228 (gemm_cuda) and
-// :230-238 (gemm_graphsafe_cuda); both compute the same GEMM, and this
-// library's version never allocates, so both are graph-safe.
+// :230-238 (gemm_graphsafe_cuda); both compute the same GEMM.  Below 256
+// tokens this library's weight-streaming kernel runs; from 256 up, hipBLASLt
+// (no workspace).  Neither allocates device memory per call, so both are
+// graph-safe once a shape has been called outside the capture (its first call
+// on a device makes the hipBLASLt handle and plan).
 PEGA_API int gemm_cuda(const uint16_t* W, const uint16_t* X, uint16_t* Y, int M, int N, int K,
                        hipStream_t stream) {
-  return dense_launch<false>(W, X, Y, M, M, N, K, stream, "gemm_cuda");
+  return dense_gemm_bf16(W, X, Y, M, N, K, stream, "gemm_cuda");
 }
 
 PEGA_API int gemm_graphsafe_cuda(const uint16_t* W, const uint16_t* X, uint16_t* Y, int M, int N,
                                  int K, hipStream_t stream) {
-  return dense_launch<false>(W, X, Y, M, M, N, K, stream, "gemm_graphsafe_cuda");
+  return dense_gemm_bf16(W, X, Y, M, N, K, stream, "gemm_graphsafe_cuda");
 }
 
 // No reference counterpart as one symbol: the shared expert's gate/up GEMM

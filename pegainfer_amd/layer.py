@@ -209,8 +209,13 @@ class KimiSharedExpert:
     """The Kimi-K2 shared expert, a bf16 dense MLP (moe_nccl.rs:107-123): gate/up
     GEMM [2I, H] -> SwiGLU (gate first; silu_mul_fused_cuda,
     csrc/shared/fused_proj.cu:11-31) -> down GEMM [H, I], bf16 `projected` out.
-    The gate/up GEMM and the SwiGLU run as one launch (dense_w13_swiglu, the same
-    bits as the reference's two calls)."""
+    At decode sizes the gate/up GEMM and the SwiGLU run as one launch
+    (dense_w13_swiglu, the same bits as the reference's two calls); from
+    PREFILL_TOKENS tokens the reference's prefill sequence runs instead
+    (moe_nccl.rs:266-275): the gate/up GEMM into [T, 2I] (gemm_graphsafe, which
+    takes hipBLASLt at those sizes), the SwiGLU kernel, the down GEMM."""
+
+    PREFILL_TOKENS = 256
 
     def __init__(self, gate_up: torch.Tensor, down: torch.Tensor, *, max_tokens: int,
                  device="cuda"):
@@ -221,10 +226,16 @@ class KimiSharedExpert:
         assert tuple(down.shape) == (self.H, self.I)
         bf = dict(dtype=torch.bfloat16, device=device)
         self.act = torch.zeros(max_tokens, self.I, **bf)
+        self.h13 = (torch.zeros(max_tokens, 2 * self.I, **bf)
+                    if max_tokens >= self.PREFILL_TOKENS else None)
 
     def forward(self, normed: torch.Tensor, projected: torch.Tensor) -> torch.Tensor:
         T = normed.shape[0]
-        ops.dense_w13_swiglu(self.gate_up, normed, self.act[:T])
+        if T >= self.PREFILL_TOKENS:
+            ops.gemm_graphsafe(self.gate_up, normed, self.h13[:T])
+            ops.kimi_marlin_w13_swiglu(self.h13[:T], self.act[:T], T, self.I)
+        else:
+            ops.dense_w13_swiglu(self.gate_up, normed, self.act[:T])
         ops.gemm_graphsafe(self.down, self.act[:T], projected)
         return projected
 

@@ -191,13 +191,22 @@ def test_dense_w13_swiglu_three_and_four_token_blocks(oracle, I, N, K, rb):
     g = np.random.default_rng(I + N + K)
     w = dev(oracle.f32_to_bf16((g.standard_normal((2 * I, K)) * 0.02).astype(np.float32)))
     x = dev(oracle.f32_to_bf16(g.standard_normal((N, K)).astype(np.float32)))
-    gu = torch.zeros(N, 2 * I, dtype=torch.bfloat16, device="cuda")
-    ops.gemm_graphsafe(w, x, gu)
-    chain = torch.zeros(N, I, dtype=torch.bfloat16, device="cuda")
-    ops.kimi_marlin_w13_swiglu(gu, chain, N, I)
     fused = torch.full((N, I), float("nan"), dtype=torch.bfloat16, device="cuda")
     ops.dense_w13_swiglu(w, x, fused)
-    assert np.array_equal(host(fused), host(chain))
+    if N < 256:
+        # the two-call chain runs the same GEMM kernel: the same bits
+        gu = torch.zeros(N, 2 * I, dtype=torch.bfloat16, device="cuda")
+        ops.gemm_graphsafe(w, x, gu)
+        chain = torch.zeros(N, I, dtype=torch.bfloat16, device="cuda")
+        ops.kimi_marlin_w13_swiglu(gu, chain, N, I)
+        assert np.array_equal(host(fused), host(chain))
+    else:
+        # from 256 tokens gemm_graphsafe takes hipBLASLt (another summation order): the
+        # fused launch against the oracle's GEMM + SwiGLU on sampled tokens instead
+        g2 = np.random.default_rng(1)
+        rows = np.unique(np.concatenate([[0, N - 1], g2.integers(0, N, 14)]))
+        ref = oracle.swiglu(oracle.dense_gemm(host(w), host(x)[rows]), I)
+        assert_bf16_close(host(fused)[rows], ref, what="fused dense SwiGLU")
 
 
 @pytest.mark.parametrize("M,N,K", [(7168, 64, 2048), (4096, 57, 1024)])
@@ -217,3 +226,59 @@ def test_dense_gemm_decode_sized_token_halves(oracle, M, N, K):
     xe = oracle.f32_to_bf16(g.integers(-3, 4, (N, K)).astype(np.float32))
     ref = oracle.bf16_to_f32(xe).astype(np.float32) @ oracle.bf16_to_f32(we).astype(np.float32).T
     assert np.array_equal(_gemm(we, xe), oracle.f32_to_bf16(ref))
+
+
+@pytest.mark.parametrize("M,N,K", [(4096, 256, 1024), (2048, 300, 512), (7168, 512, 2048),
+                                   (4096, 4096, 7168)])
+def test_dense_gemm_prefill_sizes_sampled_rows(oracle, M, N, K):
+    """From 256 tokens the dense GEMM runs on hipBLASLt; its rows against the oracle on a
+    sample of tokens (the first, the last and a seeded spread), at the Kimi shared
+    expert's gate/up shape at 4096 tokens among them."""
+    g = np.random.default_rng(M + N + K)
+    w = oracle.f32_to_bf16((g.standard_normal((M, K)) * 0.02).astype(np.float32))
+    x = oracle.f32_to_bf16(g.standard_normal((N, K)).astype(np.float32))
+    y = _gemm(w, x)
+    rows = np.unique(np.concatenate([[0, N - 1], g.integers(0, N, 14)]))
+    assert_bf16_close(y[rows], oracle.dense_gemm(w, x[rows]), what=f"dense {M}x{N}x{K}")
+
+
+def test_dense_gemm_prefill_exact_when_partial_sums_are_exact(oracle):
+    g = np.random.default_rng(13)
+    M, N, K = 256, 320, 640
+    w = oracle.f32_to_bf16(np.ldexp(g.integers(-8, 8, (M, K)), g.integers(-4, 2, (M, K)))
+                           .astype(np.float32))
+    x = oracle.f32_to_bf16(g.integers(-6, 7, (N, K)).astype(np.float32))
+    assert np.array_equal(_gemm(w, x), oracle.dense_gemm(w, x))
+
+
+def test_kimi_shared_expert_prefill_path(oracle):
+    """The shared expert at 4096 tokens (gate/up GEMM, SwiGLU kernel, down GEMM: the
+    reference's prefill sequence) against the oracle's chain on sampled tokens, and its
+    replay in a HIP graph equal to the eager result."""
+    from pegainfer_amd import layer
+    g = np.random.default_rng(21)
+    T, H, SI = 4096, 7168, 2048
+    gu = oracle.f32_to_bf16((g.standard_normal((2 * SI, H)) * 0.02).astype(np.float32))
+    dn = oracle.f32_to_bf16((g.standard_normal((H, SI)) * 0.02).astype(np.float32))
+    normed = oracle.f32_to_bf16(g.standard_normal((T, H)).astype(np.float32))
+    shared = layer.KimiSharedExpert(dev(gu), dev(dn), max_tokens=T)
+    x = dev(normed)
+    out = torch.zeros(T, H, dtype=torch.bfloat16, device="cuda")
+    shared.forward(x, out)
+    torch.cuda.synchronize()
+    got = host(out)
+    rows = np.unique(np.concatenate([[0, T - 1], g.integers(0, T, 6)]))
+    # each stage against the oracle given the GPU's own input to it: the gate/up GEMM, the
+    # SwiGLU (exact), the down GEMM
+    h13 = host(shared.h13)[rows]
+    assert_bf16_close(h13, oracle.dense_gemm(gu, normed[rows]), what="shared gate/up")
+    act = host(shared.act)[rows]
+    assert np.array_equal(act, oracle.swiglu(h13, SI))
+    assert_bf16_close(got[rows], oracle.dense_gemm(dn, act), what="shared down")
+    graph = layer.capture_graph(lambda: shared.forward(x, out))
+    for _ in range(2):
+        out.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(host(out), got)
