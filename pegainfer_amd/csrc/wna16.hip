@@ -677,8 +677,9 @@ void launch_decode_pair(const GemmArgs& args, int max_m_blocks, hipStream_t stre
 
 // ---------------------------------------------------------------------------
 // Prefill kernel: one workgroup per (leader m-block, 4 column tiles); the
-// leader takes up to 128/bs consecutive m-blocks of the same expert (a
-// 128-row tile), 4 waves each own one 64-column tile.
+// leader takes up to R/bs consecutive m-blocks of the same expert (an R-row
+// tile, R = 128, or 64 where experts hold few rows), 4 waves each own one
+// 64-column tile.
 //
 // Per 64-wide K chunk (two quant groups):
 //   * activations: 128 rows x 64 k (16 KB) staged in double-buffered LDS
@@ -693,25 +694,29 @@ void launch_decode_pair(const GemmArgs& args, int max_m_blocks, hipStream_t stre
 // before weight loads so that waiting for the former leaves the latter in
 // flight (vector-memory counters retire in order).
 // ---------------------------------------------------------------------------
-constexpr int kPfRows = 128;
 constexpr int kPfChunk = 64;                 // k per LDS stage (2 quant groups)
 constexpr int kPfLdsStride = kPfChunk + 8;   // bf16 per LDS row (padding vs bank conflicts)
+// bf16 elements of the LDS area of an R-row tile: the two activation stages,
+// or the epilogue's 64-row staging ([64][264] bf16, or [2][64][65] words)
+constexpr int pf_lds_elems(int R) {
+  return 2 * R * kPfLdsStride > 64 * 264 ? 2 * R * kPfLdsStride : 64 * 264;
+}
 
 struct PfB {
   u32x4_t w[2];   // per group: the 4 words (th, w = 0..3) of this lane's k-tile
   uint32_t s[2];  // per group: this lane's two column scales
 };
 
-typedef uint16_t PfStage[kPfRows * kPfLdsStride];
-
 // Main loop and epilogue of one wave for a tile with RB routed 32-row blocks
 // (RB = 0: a wave past the last column tile, which only helps stage the
 // activations).  A compile-time RB keeps every loop body branch-free and
 // allocates only the accumulators in use.
-template <int RB>
-__device__ __forceinline__ void prefill_tile(const GemmArgs& p, PfStage* s_a, uint32_t* s_w_wave,
+template <int RB, int R>
+__device__ __forceinline__ void prefill_tile(const GemmArgs& p, uint16_t* s_a, uint32_t* s_w_wave,
                                              const int* s_sid, const float* s_tw, int expert,
                                              int nt, int tx) {
+  constexpr int kStage = R * kPfLdsStride;  // bf16 per activation stage
+  constexpr int kPieces = R / 32;           // 16-byte activation pieces per thread per chunk
   const int tid = threadIdx.x, lane = tid & 63;
   const int c = lane & 31, h = lane >> 5;
   const int K = p.size_k, N = p.size_n;
@@ -750,11 +755,11 @@ __device__ __forceinline__ void prefill_tile(const GemmArgs& p, PfStage* s_a, ui
     }
   };
 
-  // Activation staging: 128 rows x 64 k = 1024 16-byte pieces, 4 per thread;
+  // Activation staging: R rows x 64 k = 8 R 16-byte pieces, R / 32 per thread;
   // rows not routed here read zeros (out-of-range buffer offset).
-  uint32_t a_voff[4];
+  uint32_t a_voff[kPieces];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < kPieces; ++i) {
     const int piece = tid + 256 * i;
     const int r = piece >> 3, q = piece & 7;
     const int sid = s_sid[r];
@@ -763,18 +768,19 @@ __device__ __forceinline__ void prefill_tile(const GemmArgs& p, PfStage* s_a, ui
                     : kOutOfRange;
   }
   // A chunk index past the end reads zeros (every lane out of range).
-  auto load_a = [&](u32x4_t (&st)[4], int chunk) {
+  auto load_a = [&](u32x4_t (&st)[kPieces], int chunk) {
     const uint32_t past = chunk < chunks ? 0u : kOutOfRange;
     const uint32_t ch = static_cast<uint32_t>(min(chunk, chunks - 1));
 #pragma unroll
-    for (int i = 0; i < 4; ++i) st[i] = buf_load_b128(ar, a_voff[i] | past, ch * (kPfChunk * 2u));
+    for (int i = 0; i < kPieces; ++i)
+      st[i] = buf_load_b128(ar, a_voff[i] | past, ch * (kPfChunk * 2u));
   };
-  auto store_a = [&](const u32x4_t (&st)[4], int buf) {
+  auto store_a = [&](const u32x4_t (&st)[kPieces], int buf) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < kPieces; ++i) {
       const int piece = tid + 256 * i;
       const int r = piece >> 3, q = piece & 7;
-      *reinterpret_cast<u32x4_t*>(&s_a[buf][r * kPfLdsStride + 8 * q]) = st[i];
+      *reinterpret_cast<u32x4_t*>(&s_a[buf * kStage + r * kPfLdsStride + 8 * q]) = st[i];
     }
   };
 
@@ -801,7 +807,7 @@ __device__ __forceinline__ void prefill_tile(const GemmArgs& p, PfStage* s_a, ui
         const BFrags f = make_b(w4, b.s[gg], dq);
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
-          const uint16_t* ap = &s_a[buf][(32 * rb + c) * kPfLdsStride + 32 * gg + 16 * h];
+          const uint16_t* ap = &s_a[buf * kStage + (32 * rb + c) * kPfLdsStride + 32 * gg + 16 * h];
           const bf16x8_t A1 = *reinterpret_cast<const bf16x8_t*>(ap);
           const bf16x8_t A2 = *reinterpret_cast<const bf16x8_t*>(ap + 8);
           accx[rb] = mfma(A1, f.x1, accx[rb]);
@@ -814,7 +820,7 @@ __device__ __forceinline__ void prefill_tile(const GemmArgs& p, PfStage* s_a, ui
   };
 
   PfB b_even, b_odd;
-  u32x4_t st_even[4], st_odd[4];
+  u32x4_t st_even[kPieces], st_odd[kPieces];
   load_a(st_even, 0);
   load_b(b_even, 0);
   load_a(st_odd, 1);
@@ -860,7 +866,7 @@ __device__ __forceinline__ void prefill_tile(const GemmArgs& p, PfStage* s_a, ui
     const int g0 = tx * 2;  // first gate tile of this workgroup
     const int gate_tiles = p.inter >> 6;
 #pragma unroll
-    for (int ph = 0; ph < 2; ++ph) {
+    for (int ph = 0; ph < R / 64; ++ph) {
       if constexpr (RB > 0) {
         const int pair = wave & 1, half = wave >> 1;  // half 0: gate, 1: up
         const int col = (c >> 3) * 16 + (c & 7);
@@ -913,7 +919,7 @@ __device__ __forceinline__ void prefill_tile(const GemmArgs& p, PfStage* s_a, ui
   uint16_t* xo = reinterpret_cast<uint16_t*>(s_a);
   const int wave = threadIdx.x >> 6;
 #pragma unroll
-  for (int ph = 0; ph < 2; ++ph) {
+  for (int ph = 0; ph < R / 64; ++ph) {
     if constexpr (RB > 0) {
       const int col = wave * 64 + (c >> 3) * 16 + (c & 7);
 #pragma unroll
@@ -961,11 +967,12 @@ constexpr int kPfScanSlab = 1024;  // block experts staged in LDS per scan pass
 
 // One workgroup's tile of a problem: column group tx, tile ty (the ty-th
 // 128-row tile start among the routed blocks).
+template <int R>
 __device__ __forceinline__ void prefill_block(const GemmArgs& p, int tx, int ty) {
-  __shared__ __align__(16) PfStage s_a[2];
+  __shared__ __align__(16) uint16_t s_a[pf_lds_elems(R)];
   __shared__ __align__(16) uint32_t s_w[4][kSlotDwords];
-  __shared__ int s_sid[kPfRows];
-  __shared__ float s_tw[kPfRows];  // with mul: the row's top-k weight rounded to bf16
+  __shared__ int s_sid[R];
+  __shared__ float s_tw[R];  // with mul: the row's top-k weight rounded to bf16
   __shared__ int s_e[kPfScanSlab];
   __shared__ int s_tile;
 
@@ -975,7 +982,7 @@ __device__ __forceinline__ void prefill_block(const GemmArgs& p, int tx, int ty)
   if (ntp > p.sorted_len) ntp = p.sorted_len;
   const int nblocks = ntp / p.bs;
   if (ty >= nblocks) return;  // a tile starts at a distinct block
-  const int per_tile = kPfRows / p.bs;  // m-blocks per 128-row tile (>= 1)
+  const int per_tile = R / p.bs;  // m-blocks per R-row tile (>= 1)
 
   // Wave 0 carries the scan state across 64-block windows and slabs.
   int tiles_before = 0;   // tiles starting before the current window
@@ -1025,7 +1032,7 @@ __device__ __forceinline__ void prefill_block(const GemmArgs& p, int tx, int ty)
   const int rows = nb * p.bs;
 
   const int valid_limit = p.size_m * p.top_k;
-  for (int r = tid; r < kPfRows; r += blockDim.x) {
+  for (int r = tid; r < R; r += blockDim.x) {
     const int sid = (r < rows) ? p.sorted_ids[mb * p.bs + r] : valid_limit;
     s_sid[r] = sid;
     s_tw[r] = (p.mul && static_cast<unsigned>(sid) < static_cast<unsigned>(valid_limit))
@@ -1038,7 +1045,7 @@ __device__ __forceinline__ void prefill_block(const GemmArgs& p, int tx, int ty)
   // expert's padding sits at the end of its segment, so for the routing
   // kernels' output this drops exactly the padding blocks).
   const uint64_t lo_rows = __ballot(s_sid[lane] < valid_limit);
-  const uint64_t hi_rows = __ballot(s_sid[64 + lane] < valid_limit);
+  const uint64_t hi_rows = R > 64 ? __ballot(s_sid[(64 + lane) % R] < valid_limit) : 0ull;
   const int row_end = hi_rows ? 128 - __builtin_clzll(hi_rows)
                               : (lo_rows ? 64 - __builtin_clzll(lo_rows) : 0);
   // Column tiles of the four waves: four consecutive tiles, or with SwiGLU two
@@ -1055,30 +1062,40 @@ __device__ __forceinline__ void prefill_block(const GemmArgs& p, int tx, int ty)
   }
   const int rb = tile_ok ? __builtin_amdgcn_readfirstlane((row_end + 31) >> 5) : 0;
   uint32_t* s_w_wave = s_w[wave];
-  switch (rb) {
-    case 0: prefill_tile<0>(p, s_a, s_w_wave, s_sid, s_tw, expert, nt, tx); break;
-    case 1: prefill_tile<1>(p, s_a, s_w_wave, s_sid, s_tw, expert, nt, tx); break;
-    case 2: prefill_tile<2>(p, s_a, s_w_wave, s_sid, s_tw, expert, nt, tx); break;
-    case 3: prefill_tile<3>(p, s_a, s_w_wave, s_sid, s_tw, expert, nt, tx); break;
-    default: prefill_tile<4>(p, s_a, s_w_wave, s_sid, s_tw, expert, nt, tx); break;
+  if constexpr (R == 64) {
+    switch (rb) {
+      case 0: prefill_tile<0, R>(p, s_a, s_w_wave, s_sid, s_tw, expert, nt, tx); break;
+      case 1: prefill_tile<1, R>(p, s_a, s_w_wave, s_sid, s_tw, expert, nt, tx); break;
+      default: prefill_tile<2, R>(p, s_a, s_w_wave, s_sid, s_tw, expert, nt, tx); break;
+    }
+  } else {
+    switch (rb) {
+      case 0: prefill_tile<0, R>(p, s_a, s_w_wave, s_sid, s_tw, expert, nt, tx); break;
+      case 1: prefill_tile<1, R>(p, s_a, s_w_wave, s_sid, s_tw, expert, nt, tx); break;
+      case 2: prefill_tile<2, R>(p, s_a, s_w_wave, s_sid, s_tw, expert, nt, tx); break;
+      case 3: prefill_tile<3, R>(p, s_a, s_w_wave, s_sid, s_tw, expert, nt, tx); break;
+      default: prefill_tile<4, R>(p, s_a, s_w_wave, s_sid, s_tw, expert, nt, tx); break;
+    }
   }
 }
 
+template <int R>
 __global__ __launch_bounds__(256, 2) void wna16_prefill_kernel(GemmArgs p) {
-  prefill_block(p, blockIdx.x, blockIdx.y);
+  prefill_block<R>(p, blockIdx.x, blockIdx.y);
 }
 
 // Two independent problems in one launch (e.g. a layer's routed experts and
 // its shared expert): the flat grid holds the first problem's x0-by-y
 // workgroups, then the second's, each in its own x-fastest order, so one
 // stream keeps both on the GPU at once.
-__global__ __launch_bounds__(256, 2) void wna16_prefill_pair_kernel(GemmArgs p0, GemmArgs p1,
-                                                                    int x0, int n0, int x1) {
+template <int R>
+__global__ __launch_bounds__(256, 2) void wna16_prefill_pair_kernel(
+    GemmArgs p0, GemmArgs p1, int x0, int n0, int x1) {
   const int l = static_cast<int>(blockIdx.x);
   if (l < n0)
-    prefill_block(p0, l % x0, l / x0);
+    prefill_block<R>(p0, l % x0, l / x0);
   else
-    prefill_block(p1, (l - n0) % x1, (l - n0) / x1);
+    prefill_block<R>(p1, (l - n0) % x1, (l - n0) / x1);
 }
 
 // W13 finish fused with SwiGLU: for every routed row, the gate and up
@@ -1131,6 +1148,13 @@ __global__ void w13_swiglu_partials_kernel(GemmArgs p, uint16_t* __restrict__ ac
 }
 
 bool valid_block_size(int bs) { return bs == 8 || (bs >= 16 && bs <= 64 && bs % 16 == 0); }
+
+// Prefill tile height: 64 rows when the routes could fill at most 64 rows per
+// expert on average, else 128.  Few rows per expert leave the 128-row tiles
+// mostly one or two 32-row blocks anyway, while a problem's large experts (a
+// shared expert in the same pair launch) would get tiles twice as long as the
+// rest, which then set the launch's last round.
+bool small_prefill_tiles(long long routes, long long experts) { return routes <= 64LL * experts; }
 
 // The kernels address one expert's weights and the activations through
 // 32-bit buffer ranges.  The activation range must also stay at or below
@@ -1198,8 +1222,11 @@ int wna16_gemm(const uint16_t* input, uint16_t* output, float* c_tmp, long long 
     return launch_status("wna16_gemm (decode)");
   }
   if (max_m_blocks > 65535) return fail(kNotSupported, "wna16_gemm: too many m-blocks");
-  hipLaunchKernelGGL(wna16_prefill_kernel, dim3(ceil_div(n_tiles, 4), max_m_blocks), dim3(256),
-                     0, stream, args);
+  const dim3 grid(ceil_div(n_tiles, 4), max_m_blocks);
+  if (small_prefill_tiles(static_cast<long long>(size_m) * top_k, local_experts))
+    hipLaunchKernelGGL(wna16_prefill_kernel<64>, grid, dim3(256), 0, stream, args);
+  else
+    hipLaunchKernelGGL(wna16_prefill_kernel<128>, grid, dim3(256), 0, stream, args);
   return launch_status("wna16_gemm (prefill)");
 }
 
@@ -1247,8 +1274,11 @@ int wna16_w13_swiglu(const uint16_t* input, uint16_t* act, float* partials, long
                   b_scales, nullptr, sorted_token_ids, expert_ids, num_tokens_post_padded,
                   nullptr, sorted_token_ids_len, moe_block_size, top_k, 0, size_m, size_n,
                   size_k, local_experts, 1, nullptr, act, inter};
-    hipLaunchKernelGGL(wna16_prefill_kernel, dim3(ceil_div(inter / 64, 2), max_m_blocks),
-                       dim3(256), 0, stream, args);
+    const dim3 grid(ceil_div(inter / 64, 2), max_m_blocks);
+    if (small_prefill_tiles(static_cast<long long>(size_m) * top_k, local_experts))
+      hipLaunchKernelGGL(wna16_prefill_kernel<64>, grid, dim3(256), 0, stream, args);
+    else
+      hipLaunchKernelGGL(wna16_prefill_kernel<128>, grid, dim3(256), 0, stream, args);
     return launch_status("w13_swiglu (prefill)");
   }
   if (cu_count <= 0) cu_count = current_cu_count();
@@ -1367,8 +1397,16 @@ int wna16_prefill_pair(const pega_wna16_problem* first, const pega_wna16_problem
   const long long n0 = static_cast<long long>(x0) * y0, n1 = static_cast<long long>(x1) * y1;
   if (n0 + n1 > 0x7fffffffLL)
     return fail(kNotSupported, "wna16_prefill_pair: %lld workgroups exceed the grid", n0 + n1);
-  hipLaunchKernelGGL(wna16_prefill_pair_kernel, dim3(static_cast<unsigned>(n0 + n1)), dim3(256),
-                     0, stream, a0, a1, x0, static_cast<int>(n0), x1);
+  // one tile height for both problems, from their routes and experts together
+  const long long routes = static_cast<long long>(a0.size_m) * a0.top_k +
+                           static_cast<long long>(a1.size_m) * a1.top_k;
+  const dim3 grid(static_cast<unsigned>(n0 + n1));
+  if (small_prefill_tiles(routes, static_cast<long long>(a0.num_experts) + a1.num_experts))
+    hipLaunchKernelGGL(wna16_prefill_pair_kernel<64>, grid, dim3(256), 0, stream, a0, a1, x0,
+                       static_cast<int>(n0), x1);
+  else
+    hipLaunchKernelGGL(wna16_prefill_pair_kernel<128>, grid, dim3(256), 0, stream, a0, a1, x0,
+                       static_cast<int>(n0), x1);
   return launch_status("wna16_prefill_pair");
 }
 

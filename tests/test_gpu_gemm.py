@@ -400,6 +400,53 @@ def test_prefill_pair_matches_single_launches(oracle, first, second):
             assert (ref == 0x40A0).all(axis=1).any(), "rows of other GPUs' routes keep bf16(5.0)"
 
 
+@pytest.mark.parametrize("bs", [32, 48, 64])
+@pytest.mark.parametrize("swiglu", [False, True])
+def test_prefill_tile_heights_agree(oracle, bs, swiglu):
+    """The prefill kernel runs 64-row tiles when the routes could fill at most 64 rows
+    per expert and 128-row tiles otherwise; every output's sum is the same MFMA sequence
+    in either.  The tile height follows (routes, expert count), so the same problem goes
+    through the shape-general entries with its real expert count (400 routes over 4
+    experts: 128-row tiles) and with a larger count no route uses (64-row tiles); exact
+    data, so both equal the oracle bit for bit."""
+    from pegainfer_amd import _lib, ops
+    from pegainfer_amd.ops import _ptr, _stream
+    g = np.random.default_rng(bs + 7 * swiglu)
+    E, N, K, T, topk = 4, 256, 512, 200, 2
+    q = g.integers(-8, 8, size=(E, N, K))
+    scale_bits = oracle.f32_to_bf16(np.ldexp(1.0, g.integers(-6, 1, size=(E, N, K // 32))).astype(np.float32))
+    a_bits = oracle.f32_to_bf16(g.integers(-4, 5, size=(T, K)).astype(np.float32))
+    idx = g.integers(0, E, size=(T, topk)).astype(np.int32)
+    w, packed = _setup(E, N, K, q, scale_bits)
+    ws = ops.KimiMarlinRouteWorkspace(T, bs, topk=topk, local_experts=E)
+    r = ops.moe_align_block_size(ws, dev(idx.reshape(-1)), T, T, 0)
+    a = dev(a_bits)
+    tw = dev(np.ones(T * topk, np.float32))
+    width = N // 2 if swiglu else N
+    outs = []
+    for experts in (E, 16 * E):
+        out = torch.full((T * topk, width), 7.0, dtype=torch.bfloat16, device="cuda")
+        if swiglu:
+            _lib.call("pega_wna16_w13_swiglu", _ptr(a), _ptr(out), None, 0,
+                      _ptr(w.weight_packed_uint4b8), _ptr(w.weight_scale_permuted),
+                      _ptr(r.sorted_token_ids), _ptr(r.expert_ids), _ptr(r.num_tokens_post_padded),
+                      r.sorted_token_ids.numel(), bs, topk, T, N // 2, K, experts, 32, 0, _stream())
+        else:
+            _lib.call("pega_wna16_gemm", _ptr(a), _ptr(out), None, 0, _ptr(w.weight_packed_uint4b8),
+                      _ptr(w.weight_scale_permuted), None, 0, _ptr(r.sorted_token_ids),
+                      _ptr(r.expert_ids), _ptr(r.num_tokens_post_padded), _ptr(tw),
+                      r.max_padded_tokens, bs, topk, False, T, N, K, experts, 32, 0, _stream())
+        outs.append(host(out))
+    assert np.array_equal(outs[0], outs[1])
+    routing = {k: host(v) for k, v in (("sorted_token_ids", r.sorted_token_ids),
+                                       ("expert_ids", r.expert_ids),
+                                       ("num_tokens_post_padded", r.num_tokens_post_padded))}
+    ref = oracle.wna16_gemm(a_bits, packed, scale_bits, routing, np.ones((T, topk), np.float32),
+                            moe_block_size=bs, top_k=topk, mul_topk_weights=False, size_m=T,
+                            size_n=N, size_k=K, output=np.zeros((T * topk, N), np.uint16), threads=8)
+    assert np.array_equal(outs[0], oracle.swiglu(ref, N // 2) if swiglu else ref)
+
+
 @pytest.mark.parametrize("bs,K", [(8, 2080), (16, 1056)])
 def test_gemm_decode_accepts_k_multiple_of_32(oracle, bs, K):
     """The reference accepts any K that is a multiple of 16 and of the group size 32
