@@ -265,6 +265,17 @@ int add_cuda(const uint16_t* a, const uint16_t* b, uint16_t* out, int n, hipStre
 int pega_moe_join_routed_shared_bf16(const float* routed, const uint16_t* shared, uint16_t* out,
                                      int n, hipStream_t stream);
 
+/* No reference symbol of its own: pega_moe_combine_local_f32 then
+ * pega_moe_join_routed_shared_bf16 in one pass, for a layer whose routed sum needs no
+ * reduction across GPUs between the two (one GPU holds every routed expert):
+ * out[t] = bf16(f(bf16(combine_t)) + f(shared[t])), where combine_t is the fp32 sum (topk_weight
+ * NULL) or fmaf chain over the token's local routes, k ascending from +0 -- the same bits as
+ * the two calls.  hidden_dim % 8 == 0, 16-byte aligned buffers. */
+int pega_moe_combine_join_bf16(const uint16_t* route_output, const int32_t* topk_idx,
+                               const float* topk_weight, const uint16_t* shared, uint16_t* out,
+                               int active_tokens, int topk, int hidden_dim, int global_start,
+                               int local_experts, hipStream_t stream);
+
 /* ---------------- dense bf16 GEMM (shared expert) ----------------
  * Y[n][m] = bf16(sum_k W[m][k] * X[n][k]) with fp32 accumulation; W [M][K],
  * X [N][K], Y [N][M] bf16 row-major (the reference's cublasGemmEx(OP_T, OP_N)

@@ -60,6 +60,7 @@ SIGNATURES = {
     "f32_to_bf16_cuda": [_P, _P, _I, _P],
     "add_cuda": [_P, _P, _P, _I, _P],
     "pega_moe_join_routed_shared_bf16": [_P, _P, _P, _I, _P],
+    "pega_moe_combine_join_bf16": [_P] * 5 + [_I] * 5 + [_P],
     "pega_kimi_router_select": [_P, _P, _P, _P, _I, _I, _I, _F, _P],
     "kimi_k2_router_noaux_tc_cuda": [_P] * 6 + [_I] * 5 + [_F, _P],
     "pega_dsv2_router_select": [_P, _P, _P, _I, _I, _I, _P],

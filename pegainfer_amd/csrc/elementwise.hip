@@ -13,6 +13,7 @@
 //   f32_to_bf16_cuda                      shared/elementwise.cu:235-244,722-728
 //   add_cuda                              shared/elementwise.cu:9-21,500-507
 //   pega_moe_join_routed_shared_bf16      the two calls above in one pass
+//   pega_moe_combine_join_bf16            pega_moe_combine_local_f32 then the join, one pass
 #include "common.h"
 #include "pega_moe.h"
 
@@ -140,11 +141,14 @@ __global__ void weighted_topk_sum_kernel(const uint16_t* __restrict__ route,
 constexpr int kCombineThreads = 128;
 constexpr int kCombineCols = kCombineThreads * 8;
 
-template <bool kWeighted, int kTopk>
+// kJoin: instead of the fp32 row, write bf16(f(bf16(sum)) + f(shared)) to
+// joined (the DeepSeek-V2-Lite routed + shared join, the same two roundings).
+template <bool kWeighted, int kTopk, bool kJoin = false>
 __global__ __launch_bounds__(kCombineThreads) void combine_local_rows_kernel(
     const uint16_t* __restrict__ route, const int32_t* __restrict__ topk_idx,
     const float* __restrict__ weights, float* __restrict__ out, int topk_rt, int hidden,
-    int chunks, int global_start, int local_experts) {
+    int chunks, int global_start, int local_experts, const uint16_t* __restrict__ shared = nullptr,
+    uint16_t* __restrict__ joined = nullptr) {
   constexpr int kMaxK = kTopk > 0 ? kTopk : 1;
   const int topk = kTopk > 0 ? kTopk : topk_rt;
   const long long t = blockIdx.x / chunks;
@@ -152,6 +156,8 @@ __global__ __launch_bounds__(kCombineThreads) void combine_local_rows_kernel(
   if (d8 >= hidden) return;
   const int32_t* idx = topk_idx + t * topk;
   const uint16_t* rows = route + t * topk * hidden + d8;
+  uint4 sv = make_uint4(0, 0, 0, 0);
+  if (kJoin) sv = *reinterpret_cast<const uint4*>(shared + t * hidden + d8);  // in flight early
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   auto add = [&](const uint4& v, float wk) {
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
@@ -197,29 +203,42 @@ __global__ __launch_bounds__(kCombineThreads) void combine_local_rows_kernel(
           kWeighted ? weights[t * topk + k] : 0.0f);
     }
   }
+  if (kJoin) {
+    const uint32_t sw[4] = {sv.x, sv.y, sv.z, sv.w};
+    uint32_t ow[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint16_t lo = f2bf(__fadd_rn(bf2f(f2bf(acc[2 * j])), bf_lo(sw[j])));
+      const uint16_t hi = f2bf(__fadd_rn(bf2f(f2bf(acc[2 * j + 1])), bf_hi(sw[j])));
+      ow[j] = static_cast<uint32_t>(lo) | (static_cast<uint32_t>(hi) << 16);
+    }
+    *reinterpret_cast<uint4*>(joined + t * hidden + d8) = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+    return;
+  }
   float4* o = reinterpret_cast<float4*>(out + t * hidden + d8);
   o[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
   o[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
 }
 
-template <bool kWeighted>
+template <bool kWeighted, bool kJoin = false>
 void launch_combine_local(const uint16_t* route, const int32_t* topk_idx, const float* weights,
                           float* out, int tokens, int topk, int hidden, int global_start,
-                          int local_experts, hipStream_t stream) {
+                          int local_experts, hipStream_t stream, const uint16_t* shared = nullptr,
+                          uint16_t* joined = nullptr) {
   const int chunks = ceil_div(hidden, kCombineCols);
   const dim3 grid(static_cast<unsigned>(static_cast<long long>(tokens) * chunks));
   if (topk == 8)
-    hipLaunchKernelGGL((combine_local_rows_kernel<kWeighted, 8>), grid, dim3(kCombineThreads), 0,
-                       stream, route, topk_idx, weights, out, topk, hidden, chunks, global_start,
-                       local_experts);
+    hipLaunchKernelGGL((combine_local_rows_kernel<kWeighted, 8, kJoin>), grid,
+                       dim3(kCombineThreads), 0, stream, route, topk_idx, weights, out, topk,
+                       hidden, chunks, global_start, local_experts, shared, joined);
   else if (topk == 6)
-    hipLaunchKernelGGL((combine_local_rows_kernel<kWeighted, 6>), grid, dim3(kCombineThreads), 0,
-                       stream, route, topk_idx, weights, out, topk, hidden, chunks, global_start,
-                       local_experts);
+    hipLaunchKernelGGL((combine_local_rows_kernel<kWeighted, 6, kJoin>), grid,
+                       dim3(kCombineThreads), 0, stream, route, topk_idx, weights, out, topk,
+                       hidden, chunks, global_start, local_experts, shared, joined);
   else
-    hipLaunchKernelGGL((combine_local_rows_kernel<kWeighted, 0>), grid, dim3(kCombineThreads), 0,
-                       stream, route, topk_idx, weights, out, topk, hidden, chunks, global_start,
-                       local_experts);
+    hipLaunchKernelGGL((combine_local_rows_kernel<kWeighted, 0, kJoin>), grid,
+                       dim3(kCombineThreads), 0, stream, route, topk_idx, weights, out, topk,
+                       hidden, chunks, global_start, local_experts, shared, joined);
 }
 
 // out = bf16( routed*scale + f(bf16(f(hidden) + f(projected))) )
@@ -406,6 +425,36 @@ PEGA_API int pega_moe_combine_local_f32(const uint16_t* route_output, const int3
     launch_combine_local<false>(route_output, topk_idx, topk_weight, out, active_tokens, topk,
                                 hidden_dim, global_start, local_experts, stream);
   return launch_status("combine_local");
+}
+
+// No reference symbol of its own: pega_moe_combine_local_f32 followed by
+// pega_moe_join_routed_shared_bf16 (the DeepSeek-V2-Lite layer's weighted
+// combine, then f32_to_bf16 and the bf16 add with the shared expert's output,
+// nccl_backend.rs:544-545, runtime/moe.rs:656) in one pass, for a layer whose
+// routed sum needs no reduction across GPUs in between: the same fp32 chain and
+// the same two roundings, without the fp32 routed rows in HBM.
+PEGA_API int pega_moe_combine_join_bf16(const uint16_t* route_output, const int32_t* topk_idx,
+                                        const float* topk_weight, const uint16_t* shared,
+                                        uint16_t* out, int active_tokens, int topk,
+                                        int hidden_dim, int global_start, int local_experts,
+                                        hipStream_t stream) {
+  if (!route_output || !topk_idx || !shared || !out || active_tokens < 0 || topk <= 0 ||
+      hidden_dim <= 0 || local_experts <= 0)
+    return fail(kInvalidValue, "combine_join: bad arguments");
+  if (hidden_dim % 8 != 0 || !aligned16(route_output) || !aligned16(shared) || !aligned16(out))
+    return fail(kInvalidValue, "combine_join: hidden_dim %% 8 and 16-byte alignment required");
+  if (active_tokens == 0) return kSuccess;
+  if (static_cast<long long>(active_tokens) * ceil_div(hidden_dim, kCombineCols) > 0x7fffffffLL)
+    return fail(kInvalidValue, "combine_join: tokens x column chunks overflows the grid");
+  if (topk_weight)
+    launch_combine_local<true, true>(route_output, topk_idx, topk_weight, nullptr, active_tokens,
+                                     topk, hidden_dim, global_start, local_experts, stream,
+                                     shared, out);
+  else
+    launch_combine_local<false, true>(route_output, topk_idx, topk_weight, nullptr, active_tokens,
+                                      topk, hidden_dim, global_start, local_experts, stream,
+                                      shared, out);
+  return launch_status("combine_join");
 }
 
 // Reference: pegainfer-kernels/src/ffi/kimi.rs:309-317.

@@ -69,7 +69,8 @@ class RoutedExperts:
 
     def forward(self, hidden: torch.Tensor, topk_idx: torch.Tensor, topk_w: torch.Tensor,
                 out_f32: torch.Tensor, combine: str = "sum", w13_timer=None,
-                reference_flow: bool = False, companion=None, routing=None) -> torch.Tensor:
+                reference_flow: bool = False, companion=None, routing=None,
+                join=None) -> torch.Tensor:
         """Routed-expert forward (moe_nccl.rs:152-203 order: align, W13, SwiGLU, W2
         with the top-k weight, top-k combine).  W13 and SwiGLU are one call unless
         reference_flow is set.
@@ -90,7 +91,10 @@ class RoutedExperts:
         independent problems (ExpertFFN.pair_problems, a shared expert) that run in
         the same two launches as this layer's W13 and W2, dispatched first.
         `routing` (optional): the permutation of topk_idx already built in this
-        layer's route workspace (route_from_logits); the align launch is then skipped."""
+        layer's route workspace (route_from_logits); the align launch is then skipped.
+        `join` (optional, not with reference_flow): a (shared, out) pair of bf16
+        [T, H] tensors; the combine then writes out = bf16(f(bf16(combine)) + f(shared))
+        in the same launch (the DSV2 join, ops.moe_combine_join) instead of out_f32."""
         T = hidden.shape[0]
         rows = T * self.topk
         if routing is None:
@@ -136,6 +140,11 @@ class RoutedExperts:
                 ops.kimi_marlin_sum_topk_rows_f32(route_out, T, out_f32, self.topk, self.H)
             else:
                 ops.weighted_topk_sum_f32(route_out, topk_w, T, out_f32, self.topk, self.H)
+        elif join is not None:
+            shared, out = join
+            ops.moe_combine_join(route_out, topk_idx, None if weighted_in_gemm else topk_w,
+                                 shared, out, T, self.topk, self.H, self.global_start, self.E)
+            return out
         else:
             ops.moe_combine_local_f32(route_out, topk_idx, None if weighted_in_gemm else topk_w,
                                       T, out_f32, self.topk, self.H, self.global_start, self.E)
@@ -367,9 +376,10 @@ class Dsv2MoeLayer:
         if self.pair:
             companion = self.shared.pair_problems(hidden, self.shared_out[:T])
             routing = self._route(logits, T)
+            # the shared expert is done when W2's launch is, so the combine takes the join
             self.routed.forward(hidden, self.topk_idx[:T], self.topk_w[:T], self.routed_f32[:T],
-                                combine="weighted", companion=companion, routing=routing)
-            ops.moe_join_routed_shared(self.routed_f32[:T], self.shared_out[:T], out)
+                                combine="weighted", companion=companion, routing=routing,
+                                join=(self.shared_out[:T], out))
             return out
         main = torch.cuda.current_stream()
         if self.overlap_shared and self.side is None:

@@ -614,6 +614,26 @@ def moe_join_routed_shared(routed_f32: torch.Tensor, shared: torch.Tensor,
               _stream())
 
 
+def moe_combine_join(route_output: torch.Tensor, topk_idx: torch.Tensor, topk_weight,
+                     shared: torch.Tensor, out: torch.Tensor, active_tokens: int, topk: int,
+                     hidden: int, global_start: int, local_experts: int) -> None:
+    """moe_combine_local_f32 then moe_join_routed_shared in one launch (no fp32 rows in
+    between), for a layer whose routed sum needs no cross-GPU reduction before the
+    join: out = bf16(f(bf16(combine)) + f(shared)), the same bits as the two calls."""
+    _ensure(route_output.numel() >= active_tokens * topk * hidden and _is_bf16(route_output),
+            "route_output must be bf16 [tokens * topk, hidden]")
+    _ensure(topk_idx.dtype == torch.int32 and topk_idx.numel() >= active_tokens * topk,
+            "topk_idx must be int32 [tokens, topk]")
+    _ensure(topk_weight is None or (topk_weight.dtype == torch.float32 and
+                                    topk_weight.numel() >= active_tokens * topk),
+            "topk_weight must be float32 [tokens, topk]")
+    _ensure(_is_bf16(shared) and _is_bf16(out) and shared.numel() >= active_tokens * hidden
+            and out.numel() >= active_tokens * hidden, "shared / out must be bf16 [tokens, hidden]")
+    _lib.call("pega_moe_combine_join_bf16", _ptr(route_output), _ptr(topk_idx),
+              None if topk_weight is None else _ptr(topk_weight), _ptr(shared), _ptr(out),
+              active_tokens, topk, hidden, global_start, local_experts, _stream())
+
+
 # --------------------------------------------------------------------------
 # Dense bf16 GEMM (the shared expert's projections)
 # --------------------------------------------------------------------------

@@ -116,6 +116,13 @@ def test_combine_local_equals_zero_filled_combine(oracle, T, topk, H, gs, E, wei
            else oracle.sum_topk_rows(r_zero, T, topk, H))
     got = host(out)
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    # the same combine with the DSV2 join in one launch: the two-rounding join of ref
+    sh = _bf16_rand(g, (T, H), 4.0)
+    joined = torch.full((T, H), 5.0, dtype=torch.bfloat16, device="cuda")
+    ops.moe_combine_join(dev(r_garbage), dev(idx), dev(w) if weighted else None, dev(sh), joined,
+                         T, topk, H, gs, E)
+    want = oracle.dsv2_join(ref.reshape(-1), sh.reshape(-1)).reshape(T, H)
+    assert np.array_equal(host(joined), want)
 
 
 def test_residual_joins_bit_exact(oracle):

@@ -193,10 +193,10 @@ def test_c4_dsv2_layer(oracle):
                              mul_topk_weights=False, size_m=T * topk, size_n=H, size_k=I,
                              threads=16)
     assert_bf16_close(ro, ref2, what="C4 W2")
-    routed_f32 = host(moe.routed_f32)
-    assert np.array_equal(routed_f32, oracle.weighted_topk_sum(ro, ref_w, T, topk, H))
+    routed_f32 = oracle.weighted_topk_sum(ro, ref_w, T, topk, H)
     sh = host(moe.shared_out)
-    # the join as the reference rounds it: bf16(f(bf16(routed)) + f(shared))
+    # the combine and the join as the reference rounds them, bf16(f(bf16(routed)) + f(shared)),
+    # here in one launch
     assert np.array_equal(host(out), oracle.dsv2_join(routed_f32, sh))
     # the shared expert: one INT4 expert over all tokens (W13 + SwiGLU fused, then W2)
     sI = 2 * I
@@ -225,6 +225,8 @@ def test_c4_dsv2_layer(oracle):
     out_serial = torch.zeros_like(out)
     serial.forward(hidden_d, dev(logits), out_serial)
     assert np.array_equal(host(out_serial), host(out))
+    # the serial flow keeps the combine and the join apart: its fp32 rows are the oracle's
+    assert np.array_equal(host(serial.routed_f32), routed_f32)
 
 
 def test_c5_kimi_prefill_sampled(oracle):
