@@ -339,6 +339,11 @@ int pega_kimi_route_align(const float* logits, const float* e_score_correction_b
                           int local_experts, int block_size, int max_padded_tokens,
                           int max_m_blocks, hipStream_t stream);
 
+/* No reference counterpart: the routers' e^x, y[i] = the double-precision exp of x[i] rounded
+ * to fp32, computed as the router kernels compute it (a double polynomial, falling back to the
+ * double exp near fp32 rounding midpoints).  For tests that check it over every float. */
+int pega_exp_exact_f32(const float* x, float* y, long long n, hipStream_t stream);
+
 /* No reference symbol of its own: the DeepSeek-V2-Lite router (softmax top-k ordered by expert
  * id: pegainfer-deepseek-v2-lite/src/host_ops.rs:388-412, csrc/dsv2_lite/dsv2_lite_moe.cu:41-129)
  * followed by the token -> expert permutation, in one launch.  Outputs equal

@@ -36,6 +36,7 @@ SIGNATURES = {
     "kimi_moe_marlin_align_block_size_cuda": [_P] * 6 + [_I] * 7 + [_P],
     "pega_kimi_route_align": [_P] * 9 + [_I] * 3 + [_F] + [_I] * 5 + [_P],
     "pega_dsv2_route_align": [_P] * 8 + [_I] * 8 + [_P],
+    "pega_exp_exact_f32": [_P, _P, _LL, _P],
     "pega_moe_align_block_size": [_P] * 6 + [_I] * 7 + [_P],
     "kimi_deepep_build_marlin_routing_on_stream": [_P] * 4 + [_I] * 5 + [_P],
     "kimi_marlin_int4_reorder_weight_cuda": [_P, _P, _I, _I, _I, _I, _P],

@@ -415,6 +415,29 @@ PEGA_API int pega_kimi_router_select(const float* logits, const float* e_score_c
   return launch_status("kimi_router_select");
 }
 
+// No reference counterpart: the routers' correctly rounded e^x
+// (exp_exact_f32_fast) over n floats, so a test can hold it against the
+// double-precision exp rounded to fp32 over every float it is used on.
+namespace pega {
+namespace {
+__global__ void exp_exact_kernel(const float* __restrict__ x, float* __restrict__ y, long long n) {
+  for (long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<long long>(gridDim.x) * blockDim.x)
+    y[i] = exp_exact_f32_fast(x[i]);
+}
+}  // namespace
+}  // namespace pega
+
+PEGA_API int pega_exp_exact_f32(const float* x, float* y, long long n, hipStream_t stream) {
+  if (!x || !y || n < 0) return pega::fail(pega::kInvalidValue, "exp_exact_f32: bad arguments");
+  if (n == 0) return pega::kSuccess;
+  long long grid = (n + 255) / 256;
+  if (grid > 65536) grid = 65536;
+  hipLaunchKernelGGL(pega::exp_exact_kernel, dim3(static_cast<unsigned>(grid)), dim3(256), 0,
+                     stream, x, y, n);
+  return pega::launch_status("exp_exact_f32");
+}
+
 // The select stage and the token -> expert permutation in one launch (no
 // reference counterpart as one symbol: kimi_router.cu:20-91 followed by
 // kimi_experts.cu:197-268).  Same outputs, bit for bit, as

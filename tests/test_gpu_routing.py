@@ -374,3 +374,38 @@ def test_fused_route_align_repeated_and_graph_replays():
         torch.cuda.synchronize()
         graph.replay()
         compare(T)
+
+
+def test_router_exp_equals_double_exp_over_every_float():
+    """The routers' e^x (exp_exact_f32_fast through pega_exp_exact_f32: a double polynomial
+    that falls back to the double exp within 2^-45 of an fp32 rounding midpoint) equals the
+    device's double-precision exp rounded to fp32 (torch's float64 exp, the same device
+    library) at every float with |x| <= 80 -- about 2.2e9 values, subnormals and both zeros
+    included -- and at the values outside that range, which take the fallback."""
+    from pegainfer_amd import _lib
+    from pegainfer_amd.ops import _ptr, _stream
+    top = int(np.array([80.0], np.float32).view(np.int32)[0])
+    chunk = 1 << 27
+    y = torch.empty(chunk, dtype=torch.float32, device="cuda")
+    checked = 0
+    for sign in (0, -(1 << 31)):
+        for lo in range(0, top + 1, chunk):
+            hi = min(lo + chunk, top + 1)
+            bits = (torch.arange(lo, hi, dtype=torch.int64, device="cuda") + sign).to(torch.int32)
+            x = bits.view(torch.float32)
+            _lib.call("pega_exp_exact_f32", _ptr(x), _ptr(y), hi - lo, _stream())
+            want = torch.exp(x.double()).float()
+            got = y[:hi - lo]
+            bad = (got.view(torch.int32) != want.view(torch.int32)).sum().item()
+            assert bad == 0, f"{bad} mismatches in [{lo:#x}, {hi:#x}) sign {sign}"
+            checked += hi - lo
+    assert checked > 2_200_000_000
+    outside = torch.tensor([80.5, -80.5, 88.7, 89.0, -103.0, -104.0, 1e30, -1e30,
+                            float("inf"), float("-inf")], dtype=torch.float32, device="cuda")
+    out = torch.empty_like(outside)
+    _lib.call("pega_exp_exact_f32", _ptr(outside), _ptr(out), outside.numel(), _stream())
+    assert torch.equal(out.view(torch.int32), torch.exp(outside.double()).float().view(torch.int32))
+    nan = torch.tensor([float("nan")], dtype=torch.float32, device="cuda")
+    _lib.call("pega_exp_exact_f32", _ptr(nan), _ptr(out), 1, _stream())
+    assert torch.isnan(out[0]).item()
+
