@@ -682,7 +682,7 @@ def main():
     roof_mfma = None
     if "c5" in results:
         c5 = results["c5"]
-        roof_mfma = dict(bound="mfma", kernel="wna16_prefill_kernel (W13 with SwiGLU epilogue, C5)",
+        roof_mfma = dict(bound="mfma", kernel="wna16_prefill_kernel<128> (W13 with SwiGLU epilogue, C5)",
                          achieved=round(c5["w13_tflops"], 1), peak=BF16_PEAK_TFLOPS,
                          unit="TFLOP/s", frac=round(c5["w13_tflops"] / BF16_PEAK_TFLOPS, 4),
                          algorithmic_flops_per_launch=c5["w13_flops"],
