@@ -117,11 +117,15 @@ __device__ __forceinline__ void align_workgroup(
   //    the segment sizes across experts
   int count = 0;
   if (t < E) {
+    // all sixteen counts in flight first, then the scan in registers
+    uint32_t c[kAlignWaves];
+#pragma unroll
+    for (int w = 0; w < kAlignWaves; ++w) c[w] = cnt[w * E + t];
     uint32_t run = 0;
+#pragma unroll
     for (int w = 0; w < kAlignWaves; ++w) {
-      const uint32_t c = cnt[w * E + t];
       cnt[w * E + t] = run;
-      run += c;
+      run += c[w];
     }
     count = static_cast<int>(run);
   }
@@ -140,9 +144,11 @@ __device__ __forceinline__ void align_workgroup(
     seg_start[t] = start;
     expert_offsets[t] = static_cast<uint32_t>(start);
     expert_cursor[t] = static_cast<uint32_t>(count);
-    // sentinels on this segment's padding
+    // sentinels on this segment's padding, and the expert of each of its blocks
     for (int q = start + count; q < start + padded && q < max_padded_tokens; ++q)
       sorted_token_ids[q] = route_elems;
+    for (int b = start / block_size; b < (start + padded) / block_size && b < max_m_blocks; ++b)
+      expert_ids[b] = t;
   }
   if (t == 0) {
     seg_start[E] = total;
@@ -172,12 +178,11 @@ __device__ __forceinline__ void align_workgroup(
     }
   }
 
-  // 4. sentinels past the total; expert id per block
+  // 4. sentinels past the total; no expert past it (each segment's blocks were
+  //    written by their expert's thread above)
   for (int q = total + t; q < max_padded_tokens; q += kAlignThreads) sorted_token_ids[q] = route_elems;
-  for (int blk = t; blk < max_m_blocks; blk += kAlignThreads) {
-    const int slot = blk * block_size;
-    expert_ids[blk] = slot < total ? segment_of(seg_start, E, slot) : -1;
-  }
+  for (int blk = total / block_size + t; blk < max_m_blocks; blk += kAlignThreads)
+    expert_ids[blk] = -1;
 }
 
 

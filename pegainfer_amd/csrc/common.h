@@ -79,9 +79,13 @@ __device__ __forceinline__ float exp_exact_f32(float x) {
 // Both then round to the same float f = RN(a) unless a rounding midpoint of
 // f's neighbourhood lies within g of a: that is checked exactly (a - f is exact
 // in double), and only then, about once in 2^20 calls, does the double exp run.
-__device__ __forceinline__ float exp_exact_f32_fast(float x) {
-  if (!(__builtin_fabsf(x) <= 80.0f)) return exp_exact_f32(x);  // NaN too
-  const double xd = static_cast<double>(x);
+// exp_exact_f32_try is that fast path alone, without branches: it returns f and
+// sets *ok, which is false where the double exp must decide (|x| > 80, NaN, or a
+// midpoint within g), so that callers can evaluate several exponentials side by
+// side and take the rare fallbacks afterwards.
+__device__ __forceinline__ float exp_exact_f32_try(float x, bool* ok) {
+  const bool in = __builtin_fabsf(x) <= 80.0f;  // false for NaN too
+  const double xd = in ? static_cast<double>(x) : 0.0;
   const double n = __builtin_rint(xd * 1.4426950408889634);
   double r = __builtin_fma(-n, 0x1.62e42fefa3800p-1, xd);  // ln2_hi: 43 bits, n * ln2_hi exact
   r = __builtin_fma(-n, 0x1.ef35793c76730p-45, r);          // ln2_lo
@@ -106,8 +110,14 @@ __device__ __forceinline__ float exp_exact_f32_fast(float x) {
       double, static_cast<uint64_t>(((fb >> 23) & 0xffu) + 1023u - 151u) << 52);
   const double half_dn = (fb & 0x7fffffu) ? half_up : 0.5 * half_up;
   const double g = a * 0x1p-45;
-  if (d + g < half_up && d - g > -half_dn) return f;
-  return exp_exact_f32(x);
+  *ok = in && d + g < half_up && d - g > -half_dn;
+  return f;
+}
+
+__device__ __forceinline__ float exp_exact_f32_fast(float x) {
+  bool ok;
+  const float f = exp_exact_f32_try(x, &ok);
+  return ok ? f : exp_exact_f32(x);
 }
 
 // SwiGLU of one column pair: bf16( f(bf16(g / (1 + e^-g))) * u ), g = gate,

@@ -34,10 +34,14 @@ __device__ __forceinline__ uint32_t order_key(float v) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
+// A DPP lane move with no "old" operand (bound_ctrl), so that the compiler folds
+// it into the consuming max/min as a DPP source.  Rows outside kRowMask are not
+// written by that fused instruction and keep their value, which is the value a
+// max/min of the lane with itself would give.
 template <int kCtrl, int kRowMask = 0xF>
 __device__ __forceinline__ uint32_t dpp_mov(uint32_t v) {
-  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(
-      static_cast<int>(v), static_cast<int>(v), kCtrl, kRowMask, 0xF, false));
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_mov_dpp(static_cast<int>(v), kCtrl, kRowMask, 0xF, true));
 }
 
 // Wave-wide reduction over DPP lane moves (quad swaps, half-row and row
@@ -77,21 +81,25 @@ template <int NS>
 __device__ __forceinline__ int wave_topk_ids(uint32_t (&key)[NS], int lane, int topk) {
   int my_sel = 0;
   for (int r = 0; r < topk; ++r) {
+    // the lane's best key and its lowest slot holding it, found before the
+    // reduction so that they overlap its DPP latencies
     uint32_t best = key[0];
+    int bj = 0;
 #pragma unroll
-    for (int j = 1; j < NS; ++j) best = best > key[j] ? best : key[j];
+    for (int j = 1; j < NS; ++j) {
+      const bool up = key[j] > best;
+      best = up ? key[j] : best;
+      bj = up ? j : bj;
+    }
     const uint32_t top = wave_reduce_u32(best, MaxU32{});
-    int jsel = NS;
-#pragma unroll
-    for (int j = NS - 1; j >= 0; --j)
-      if (key[j] == top) jsel = j;
-    const uint64_t holders = __ballot(jsel < NS);
+    const bool mine = best == top;
+    const uint64_t holders = __ballot(mine);
     int win;
     if (__popcll(holders) == 1) {
       const int wl = __builtin_ctzll(holders);
-      win = __builtin_amdgcn_readlane(jsel * 64 + lane, wl);
+      win = __builtin_amdgcn_readlane(bj * 64 + lane, wl);
     } else {
-      const uint32_t cand = jsel < NS ? static_cast<uint32_t>(jsel * 64 + lane) : 0xffffffffu;
+      const uint32_t cand = mine ? static_cast<uint32_t>(bj * 64 + lane) : 0xffffffffu;
       win = static_cast<int>(wave_reduce_u32(cand, MinU32{}));
     }
     const int wj = win >> 6;
@@ -105,16 +113,12 @@ __device__ __forceinline__ int wave_topk_ids(uint32_t (&key)[NS], int lane, int 
   return my_sel;
 }
 
-// Kimi router score of logit l: 1 / (1 + e^-l), e^-l rounded from a double exp.
-__device__ __forceinline__ float kimi_score(float l) {
-  return 1.0f / (1.0f + exp_exact_f32_fast(-l));
-}
-
 // Token t's selection by one wave; lane l owns experts l, l+64, ... (NS slots
-// per lane, NS * 64 >= n_experts).  Writes the token's top-k weights and
-// returns, on lane r < topk, the r-th selected id (the caller stores the ids).
-// Each selected lane recomputes its expert's score (the same function, so the
-// same bits) rather than fetching it from the owner lane every round.
+// per lane, NS * 64 >= n_experts).  The Kimi score of logit l is
+// 1 / (1 + e^-l), e^-l rounded from a double exp.  Writes the token's top-k
+// weights and returns, on lane r < topk, the r-th selected id (the caller
+// stores the ids); lane r takes its expert's score from the owner lane once,
+// after the rounds.
 template <int NS>
 __device__ __forceinline__ int kimi_select_token(const float* __restrict__ logits,
                                                  const float* __restrict__ bias,
@@ -122,14 +126,37 @@ __device__ __forceinline__ int kimi_select_token(const float* __restrict__ logit
                                                  int n_experts, int topk, float route_scale) {
   const int lane = threadIdx.x & 63;
   const float* row = logits + static_cast<long long>(t) * n_experts;
-  uint32_t key[NS];
+  // every slot's loads, then every slot's exponential side by side (the rare
+  // double-precision fallbacks after), then the scores: kimi_score's bits
+  float lg[NS], bi[NS], ex[NS], sc[NS];
+  bool ok[NS];
 #pragma unroll
   for (int j = 0; j < NS; ++j) {
     const int e = lane + 64 * j;
-    key[j] = e < n_experts ? order_key(kimi_score(row[e]) + bias[e]) : 0u;
+    lg[j] = e < n_experts ? row[e] : 0.0f;
+    bi[j] = e < n_experts ? bias[e] : 0.0f;
+  }
+#pragma unroll
+  for (int j = 0; j < NS; ++j) ex[j] = exp_exact_f32_try(-lg[j], &ok[j]);
+#pragma unroll
+  for (int j = 0; j < NS; ++j)
+    if (!ok[j]) ex[j] = exp_exact_f32(-lg[j]);
+  uint32_t key[NS];
+#pragma unroll
+  for (int j = 0; j < NS; ++j) {
+    sc[j] = 1.0f / (1.0f + ex[j]);
+    key[j] = lane + 64 * j < n_experts ? order_key(sc[j] + bi[j]) : 0u;
   }
   const int my_i = wave_topk_ids<NS>(key, lane, topk);
-  const float my_s = lane < topk ? kimi_score(row[my_i]) : 0.0f;
+  // the selected expert's score, from its owner lane's slot
+  float my_s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NS; ++j) {
+    const float v = __builtin_bit_cast(
+        float, __builtin_amdgcn_ds_bpermute((my_i & 63) << 2, __builtin_bit_cast(int, sc[j])));
+    if (j == (my_i >> 6)) my_s = v;
+  }
+  if (lane >= topk) my_s = 0.0f;
   // sum in selection order, as the reference's rounds add them
   float sum = 0.0f;
   for (int r = 0; r < topk; ++r) sum += lane_value(my_s, r);
