@@ -253,10 +253,11 @@ def fused_route(tokens: int, topk: int, n_experts: int, softmax: bool = False) -
     """Whether a layer routes with the fused select + permutation launch.  Kimi
     (sigmoid): whenever its routes fit the one-workgroup sort (ops.ROUTE_ALIGN_MAX_ROUTES)
     and the expert count fits the select (at most 1024); graph-timed against the select
-    and permutation launches: 9.1 / 10.3 / 11.8 / 12.0 against 9.9 / 11.2 / 12.0 / 12.3 us
-    at 1 / 4 / 16 / 64 tokens.  DeepSeek-V2-Lite (softmax): up to 512 routes; at C4's
-    512 tokens (3072 routes) the fused launch took 14.9 against 13.9 us, its 128
-    workgroups' hand-off costing more than the second launch."""
+    and permutation launches: 7.8 / 8.6 / 10.2 / 10.4 against 8.6 / 9.4 / 10.2 / 10.3 us
+    at 1 / 4 / 16 / 64 tokens (equal from 16 tokens on; one launch less to capture).
+    DeepSeek-V2-Lite (softmax): up to 512 routes; at 512 tokens (3072 routes) the fused
+    launch took 15.3 against 13.5 us, its 128 workgroups' hand-off and one-workgroup sort
+    costing more than the second launch."""
     limit = 512 if softmax else ops.ROUTE_ALIGN_MAX_ROUTES
     return tokens * topk <= limit and n_experts <= 1024
 
