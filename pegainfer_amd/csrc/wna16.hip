@@ -756,10 +756,15 @@ __device__ __forceinline__ void prefill_tile(const GemmArgs& p, uint16_t* s_a, u
   };
 
   // Activation staging: R rows x 64 k = 8 R 16-byte pieces, R / 32 per thread;
-  // rows not routed here read zeros (out-of-range buffer offset).
-  uint32_t a_voff[kPieces];
+  // rows not routed here read zeros (out-of-range buffer offset).  A thread's
+  // piece i lies in 32-row block i, so a tile with RB < R / 32 routed blocks
+  // stages only its first RB blocks (the MFMAs read no other row); a wave past
+  // the last column tile (RB = 0) stages all of them, which covers whatever
+  // the workgroup's other waves need.
+  constexpr int kStaged = RB > 0 && RB < kPieces ? RB : kPieces;
+  uint32_t a_voff[kStaged];
 #pragma unroll
-  for (int i = 0; i < kPieces; ++i) {
+  for (int i = 0; i < kStaged; ++i) {
     const int piece = tid + 256 * i;
     const int r = piece >> 3, q = piece & 7;
     const int sid = s_sid[r];
@@ -768,16 +773,16 @@ __device__ __forceinline__ void prefill_tile(const GemmArgs& p, uint16_t* s_a, u
                     : kOutOfRange;
   }
   // A chunk index past the end reads zeros (every lane out of range).
-  auto load_a = [&](u32x4_t (&st)[kPieces], int chunk) {
+  auto load_a = [&](u32x4_t (&st)[kStaged], int chunk) {
     const uint32_t past = chunk < chunks ? 0u : kOutOfRange;
     const uint32_t ch = static_cast<uint32_t>(min(chunk, chunks - 1));
 #pragma unroll
-    for (int i = 0; i < kPieces; ++i)
+    for (int i = 0; i < kStaged; ++i)
       st[i] = buf_load_b128(ar, a_voff[i] | past, ch * (kPfChunk * 2u));
   };
-  auto store_a = [&](const u32x4_t (&st)[kPieces], int buf) {
+  auto store_a = [&](const u32x4_t (&st)[kStaged], int buf) {
 #pragma unroll
-    for (int i = 0; i < kPieces; ++i) {
+    for (int i = 0; i < kStaged; ++i) {
       const int piece = tid + 256 * i;
       const int r = piece >> 3, q = piece & 7;
       *reinterpret_cast<u32x4_t*>(&s_a[buf * kStage + r * kPfLdsStride + 8 * q]) = st[i];
@@ -820,7 +825,7 @@ __device__ __forceinline__ void prefill_tile(const GemmArgs& p, uint16_t* s_a, u
   };
 
   PfB b_even, b_odd;
-  u32x4_t st_even[kPieces], st_odd[kPieces];
+  u32x4_t st_even[kStaged], st_odd[kStaged];
   load_a(st_even, 0);
   load_b(b_even, 0);
   load_a(st_odd, 1);
