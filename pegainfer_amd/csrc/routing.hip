@@ -11,15 +11,16 @@
 // and -1 past the total.  The reference meets this order only on its
 // single-block path (< 1024 routes); its 4-launch path takes positions from an
 // atomic cursor, so the order inside an expert varies run to run.  Both paths
-// here are deterministic at every size.  Below 4096 routes it is one launch
+// here are deterministic at every size.  Below 2048 routes it is one launch
 // of one workgroup: each of the 16 waves owns a contiguous run of 64-route
 // steps; inside a step the lanes holding the same expert find each other with
 // one ballot per bit of the expert id, so a lane's rank among them is a
 // popcount.  Per-(wave, expert) counts in LDS are scanned down the wave axis
 // and across experts, and the scatter replays every step in order -- a
-// stable counting sort, bit-exact with the contract.  From 4096 routes a
-// count launch and a scatter launch with one workgroup per expert produce the
-// same bytes (the wide path below).
+// stable counting sort, bit-exact with the contract.  From 2048 routes one
+// launch of one workgroup per expert, and from 4096 a count launch and a
+// scatter launch with one workgroup per expert, produce the same bytes (the
+// per-expert and wide paths below).
 #include "align_core.h"
 #include "common.h"
 #include "pega_moe.h"
@@ -215,10 +216,136 @@ __global__ __launch_bounds__(kAlignThreads) void align_scatter_kernel(
   }
 }
 
+// One launch, one workgroup per local expert: each workgroup first counts
+// every expert's routes itself (per 64-route step, the lanes holding the same
+// expert find each other by one ballot per id bit and the lowest of them adds
+// the set's size to an LDS histogram), so no second launch has to wait for
+// the counts; then it writes its own expert's segment as the scatter kernel
+// above does.  Same bytes as the other two paths.
+__global__ __launch_bounds__(kAlignThreads) void align_expert_kernel(
+    const int32_t* __restrict__ topk_idx, int32_t* __restrict__ sorted_token_ids,
+    int32_t* __restrict__ expert_ids, int32_t* __restrict__ num_tokens_post_padded,
+    uint32_t* __restrict__ expert_offsets, uint32_t* __restrict__ expert_cursor,
+    int route_elems, int global_start, int local_experts, int block_size, int max_padded_tokens,
+    int max_m_blocks) {
+  __shared__ uint32_t s_hist[kAlignMaxExperts];
+  __shared__ int s_before[kAlignWaves], s_total[kAlignWaves], s_n[kAlignWaves];
+  const int e = blockIdx.x, t = threadIdx.x, wave = t >> 6, lane = t & 63;
+  const int E = local_experts;
+  const int key = global_start + e;
+  for (int i = t; i < E; i += kAlignThreads) s_hist[i] = 0;
+  int s0, s1;
+  wave_steps(route_elems, s0, s1);
+  const int nbits = 32 - __builtin_clz(static_cast<unsigned>(max(E - 1, 1)));
+  const uint64_t below = (1ull << lane) - 1ull;
+  // the wave's ids stay in registers when its steps fit one batch
+  const bool one_batch = s1 - s0 <= kAlignBatch;  // wave-uniform
+  int v_keep[kAlignBatch];
+  __syncthreads();
+
+  int n = 0;  // this wave's routes of expert e
+  for (int s = s0; s < s1; s += kAlignBatch) {
+    int v[kAlignBatch];
+#pragma unroll
+    for (int j = 0; j < kAlignBatch; ++j) {
+      const int r = (s + j) * 64 + lane;
+      v[j] = (s + j < s1 && r < route_elems) ? topk_idx[r] : -1;
+      v_keep[j] = v[j];
+    }
+#pragma unroll
+    for (int j = 0; j < kAlignBatch; ++j) {
+      if (s + j >= s1) continue;  // wave-uniform
+      const int le = v[j] - global_start;
+      const int ex = (v[j] >= 0 && le >= 0 && le < E) ? le : -1;
+      const uint64_t peers = same_expert_lanes(ex, nbits);
+      if (ex >= 0 && (peers & below) == 0)
+        atomicAdd(&s_hist[ex], static_cast<uint32_t>(__popcll(peers)));
+      n += __popcll(__ballot(v[j] == key));
+    }
+  }
+  __syncthreads();
+
+  // padded segment sizes of all experts: this segment's start is the sum over
+  // the experts below e, the total over all
+  int below_e = 0, all = 0, count = 0;
+  for (int i = t; i < E; i += kAlignThreads) {
+    const int c = static_cast<int>(s_hist[i]);
+    const int padded = ceil_div(c, block_size) * block_size;
+    below_e += i < e ? padded : 0;
+    all += padded;
+  }
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) {
+    below_e += __shfl_xor(below_e, d, 64);
+    all += __shfl_xor(all, d, 64);
+  }
+  if (lane == 0) {
+    s_before[wave] = below_e;
+    s_total[wave] = all;
+    s_n[wave] = n;
+  }
+  __syncthreads();
+  int start = 0, total = 0, rank = 0;
+  for (int w = 0; w < kAlignWaves; ++w) {
+    start += s_before[w];
+    total += s_total[w];
+    rank += w < wave ? s_n[w] : 0;
+    count += s_n[w];
+  }
+  const int seg_end = start + ceil_div(count, block_size) * block_size;
+
+  // this wave's routes of expert e in ascending route order, after the
+  // earlier waves'
+  for (int s = s0; s < s1; s += kAlignBatch) {
+    int v[kAlignBatch];
+#pragma unroll
+    for (int j = 0; j < kAlignBatch; ++j) {
+      const int r = (s + j) * 64 + lane;
+      v[j] = one_batch ? v_keep[j] : ((s + j < s1 && r < route_elems) ? topk_idx[r] : -1);
+    }
+#pragma unroll
+    for (int j = 0; j < kAlignBatch; ++j) {
+      if (s + j >= s1) continue;  // wave-uniform
+      const bool hit = v[j] == key;
+      const uint64_t m = __ballot(hit);
+      const int pos = start + rank + __popcll(m & below);
+      if (hit && pos < max_padded_tokens) sorted_token_ids[pos] = (s + j) * 64 + lane;
+      rank += __popcll(m);
+    }
+  }
+
+  // the segment's padding and block ids; the tail past the total is shared
+  // out over the whole grid
+  for (int q = start + count + t; q < seg_end && q < max_padded_tokens; q += kAlignThreads)
+    sorted_token_ids[q] = route_elems;
+  for (int b = start / block_size + t; b < seg_end / block_size && b < max_m_blocks;
+       b += kAlignThreads)
+    expert_ids[b] = e;
+  const int g = e * kAlignThreads + t, gstride = gridDim.x * kAlignThreads;
+  for (int q = total + g; q < max_padded_tokens; q += gstride) sorted_token_ids[q] = route_elems;
+  for (int b = total / block_size + g; b < max_m_blocks; b += gstride) expert_ids[b] = -1;
+  if (t == 0) {
+    expert_offsets[e] = static_cast<uint32_t>(start);
+    expert_cursor[e] = static_cast<uint32_t>(count);
+    if (e == 0) {
+      expert_offsets[E] = static_cast<uint32_t>(total);
+      num_tokens_post_padded[0] = total;
+    }
+  }
+}
+
 // Route counts from which the per-expert path replaces the single workgroup
 // (below it the one launch is shorter than two).
 #ifndef PEGA_ALIGN_WIDE_MIN_ROUTES
 #define PEGA_ALIGN_WIDE_MIN_ROUTES 4096
+#endif
+// From this many routes up to the wide path, the one-launch per-expert kernel
+// (graph-timed, 64 experts, 3072 routes: 7.3 against 8.5 us for the single
+// workgroup; it loses below ~2000 routes and against the two wide launches at
+// 32768 routes, 25 against 14 us, where every workgroup's full histogram costs
+// more than the second launch).
+#ifndef PEGA_ALIGN_EXPERT_MIN_ROUTES
+#define PEGA_ALIGN_EXPERT_MIN_ROUTES 2048
 #endif
 
 // Shape-general permutation (local_experts <= 512, any topk); the Kimi
@@ -248,6 +375,13 @@ int align_block_size(const int32_t* topk_idx, int32_t* sorted_token_ids, int32_t
     return fail(kInvalidValue,
                 "align_block_size: capacity too small (padded %d < %lld or blocks %d < %d)",
                 max_padded_tokens, req_padded, max_m_blocks, required_blocks);
+  if (route_elems >= PEGA_ALIGN_EXPERT_MIN_ROUTES && route_elems < PEGA_ALIGN_WIDE_MIN_ROUTES) {
+    hipLaunchKernelGGL(align_expert_kernel, dim3(local_experts), dim3(kAlignThreads), 0, stream,
+                       topk_idx, sorted_token_ids, expert_ids, num_tokens_post_padded,
+                       expert_offsets, expert_cursor, route_elems, global_start, local_experts,
+                       block_size, max_padded_tokens, max_m_blocks);
+    return launch_status("align_block_size");
+  }
   if (route_elems >= PEGA_ALIGN_WIDE_MIN_ROUTES) {
     hipLaunchKernelGGL(align_count_kernel, dim3(local_experts), dim3(kAlignThreads), 0, stream,
                        topk_idx, expert_cursor, route_elems, global_start);

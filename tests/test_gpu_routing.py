@@ -80,11 +80,12 @@ def test_align_edge_cases(oracle):
     _check_against_oracle(oracle, ws, idx, 0, 48, 16)
 
 
-@pytest.mark.parametrize("tokens", [511, 512, 513, 5000])
+@pytest.mark.parametrize("tokens", [255, 256, 257, 400, 511, 512, 513, 5000])
 def test_align_wide_path_edges(oracle, tokens):
-    """From 4096 routes the permutation runs one workgroup per expert; these
-    straddle that switch (511/512/513 tokens x top-8) and repeat the edge
-    cases at a size on the wide path."""
+    """From 2048 routes the permutation runs one workgroup per expert (one
+    launch below 4096 routes, two from there); these straddle both switches
+    (255/256/257 and 511/512/513 tokens x top-8) and repeat the edge cases on
+    each path."""
     g = np.random.default_rng(tokens)
     idx = g.integers(0, 384, size=(tokens, 8)).astype(np.int32)
     ws, _ = _gpu_align(idx, tokens, 8, 100, 48, 32)
