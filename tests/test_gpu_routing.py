@@ -104,6 +104,7 @@ def test_align_wide_path_edges(oracle, tokens):
                                               (1, 1, 9000, 64), (512, 4, 2048, 8),
                                               (8, 8, 70000, 64),
                                               (224, 8, 100, 16), (512, 8, 3000, 32),
+                                              (512, 4, 600, 8), (1, 1, 3000, 64),
                                               (37, 3, 70000, 48)])
 def test_align_general_shapes(oracle, E, topk, tokens, bs):
     g = np.random.default_rng(E + topk)
