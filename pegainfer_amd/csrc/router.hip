@@ -176,7 +176,8 @@ __global__ void kimi_router_select_kernel(const float* __restrict__ logits,
   if (t >= tokens) return;  // whole waves leave
   const int sel = kimi_select_token<NS>(logits, bias, topk_weight, t, n_experts, topk,
                                         route_scale);
-  if ((threadIdx.x & 63) < topk) topk_idx[t * topk + (threadIdx.x & 63)] = sel;
+  const int lane = static_cast<int>(threadIdx.x & 63);
+  if (lane < topk) topk_idx[t * topk + lane] = sel;
 }
 
 // DeepSeek-V2-Lite selection of token t by one wave: softmax (max-subtracted,
@@ -247,7 +248,8 @@ __global__ void dsv2_router_select_kernel(const float* __restrict__ logits,
   const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (t >= tokens) return;  // whole waves leave
   const int id = dsv2_select_token<NS>(logits, topk_weight, t, n_experts, topk);
-  if ((threadIdx.x & 63) < topk) topk_idx[t * topk + (threadIdx.x & 63)] = id;
+  const int lane = static_cast<int>(threadIdx.x & 63);
+  if (lane < topk) topk_idx[t * topk + lane] = id;
 }
 
 // Arrivals of the fused router + permutation kernel's workgroups, per device.
