@@ -141,7 +141,8 @@ int pega_wna16_gemm(const uint16_t* input, uint16_t* output, float* c_tmp, long 
  *    exactly as the W13 output is rounded.  Otherwise (or when partials is NULL or too small
  *    to split) a workgroup takes a gate tile and its up tile and applies SwiGLU in its
  *    epilogue.
- *  - Block size 32, 48 or 64 (prefill): the 128-row tile GEMM takes each gate tile and its up
+ *  - Block size 32, 48 or 64 (prefill): the tile GEMM (128-row tiles, or 64-row tiles when
+ *    the routes fill at most 64 rows per expert on average) takes each gate tile and its up
  *    tile in one workgroup and applies SwiGLU in its epilogue; partials is not used (may be
  *    NULL, partials_len 0). */
 int pega_wna16_w13_swiglu(const uint16_t* input, uint16_t* act, float* partials,
@@ -171,8 +172,8 @@ int pega_wna16_w13_swiglu_noalloc(const uint16_t* input, uint16_t* act, const ui
                                   int group_size, int sm_count, hipStream_t stream);
 
 /* One problem of pega_wna16_prefill_pair: a grouped INT4 GEMM at a prefill block size (the
- * 128-row tile kernel), as pega_wna16_gemm (act NULL) or pega_wna16_w13_swiglu (act set)
- * would run it.  Plain pointers and sizes; 112 bytes on LP64. */
+ * tile kernel), as pega_wna16_gemm (act NULL) or pega_wna16_w13_swiglu (act set) would run
+ * it.  Plain pointers and sizes; 112 bytes on LP64. */
 typedef struct pega_wna16_problem {
     const uint16_t* input;                /* bf16 [size_m, size_k], 16-byte aligned */
     uint16_t* output;                     /* bf16 [size_m * top_k, size_n] (unused with act) */
