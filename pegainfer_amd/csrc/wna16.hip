@@ -970,8 +970,11 @@ __device__ __forceinline__ void prefill_tile(const GemmArgs& p, uint16_t* s_a, u
 // over shader engines then puts all the work on half of them.)
 constexpr int kPfScanSlab = 1024;  // block experts staged in LDS per scan pass
 
-// One workgroup's tile of a problem: column group tx, tile ty (the ty-th
-// 128-row tile start among the routed blocks).
+// One workgroup's tile of a problem: column group tx, tile ty.  Up to
+// kPfScanSlab blocks, the tiles that hold all R / bs of their blocks come first
+// and the shorter last tiles of the experts after them (each group in block
+// order), so the short tiles fill the end of the launch; past that many
+// blocks, block order.
 template <int R>
 __device__ __forceinline__ void prefill_block(const GemmArgs& p, int tx, int ty) {
   __shared__ __align__(16) uint16_t s_a[pf_lds_elems(R)];
@@ -989,11 +992,51 @@ __device__ __forceinline__ void prefill_block(const GemmArgs& p, int tx, int ty)
   if (ty >= nblocks) return;  // a tile starts at a distinct block
   const int per_tile = R / p.bs;  // m-blocks per R-row tile (>= 1)
 
+  int mb = -1;
+  if (nblocks <= kPfScanSlab) {
+    for (int i = tid; i < nblocks; i += blockDim.x) s_e[i] = p.expert_ids[i];
+    if (tid == 0) s_tile = -1;
+    __syncthreads();
+    if (wave == 0) {
+      // pass 0 counts the tiles with all their blocks, pass 1 the others; an
+      // expert's blocks are contiguous, so a tile is whole when its last block
+      // has the leader's expert
+      int k = ty;
+      for (int pass = 0; pass < 2 && k >= 0; ++pass) {
+        int run_start = 0, prev_e = -1;
+        for (int w0 = 0; w0 < nblocks; w0 += 64) {
+          const int blk = w0 + lane;
+          const bool in = blk < nblocks;
+          const int e = in ? s_e[blk] : -1;
+          const int ep = lane > 0 ? s_e[blk - 1] : prev_e;
+          const uint64_t starts = __ballot(in && (blk == 0 || e != ep));
+          const uint64_t upto = starts & ((2ull << lane) - 1ull);
+          const int run = upto ? w0 + 63 - __builtin_clzll(upto) : run_start;
+          const bool lead = in && e >= 0 && e < p.num_experts && (blk - run) % per_tile == 0;
+          const int last = blk + per_tile - 1;
+          const bool whole = last < nblocks && s_e[last] == e;
+          uint64_t leads = __ballot(lead && whole == (pass == 0));
+          const int cnt = __builtin_popcountll(leads);
+          if (k < cnt) {
+            for (int q = k; q > 0; --q) leads &= leads - 1ull;
+            if (lane == 0) s_tile = w0 + __builtin_ctzll(leads);
+            k = -1;
+            break;
+          }
+          k -= cnt;
+          if (starts) run_start = w0 + 63 - __builtin_clzll(starts);
+          prev_e = s_e[min(w0 + 63, nblocks - 1)];
+        }
+      }
+    }
+    __syncthreads();
+    mb = s_tile;
+  }
   // Wave 0 carries the scan state across 64-block windows and slabs.
   int tiles_before = 0;   // tiles starting before the current window
   int run_start = 0;      // first block of the run the window starts in
   int prev_e = -1;        // expert of the block before the window (none at block 0)
-  int mb = -1;
+  if (nblocks > kPfScanSlab)
   for (int b0 = 0; b0 < nblocks; b0 += kPfScanSlab) {
     const int n = min(kPfScanSlab, nblocks - b0);
     __syncthreads();  // the previous slab is no longer read
